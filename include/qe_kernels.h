@@ -1,0 +1,149 @@
+/*
+ * qe_kernels.h — C-ABI of the MI355X (gfx950) W4A16 group-128 matrix path.
+ *
+ * One extern "C" entry point per launcher of the reference's kernel API
+ * (Areen-09/qwen-engine include/kernels.cuh).  Plain pointers and sizes only:
+ *   - fp16 buffers are `uint16_t*` (IEEE binary16 bit patterns),
+ *   - packed int4 weights are `uint32_t[N][K/8]`, nibble order
+ *     q0|q4<<4|q1<<8|q5<<12|q2<<16|q6<<20|q3<<24|q7<<28 (element 8w+j = q_j),
+ *   - group scales are fp16 `[N][K/128]`, zero point 8,
+ *   - Q8_1 activations are int8 q8[K], fp32 scale[K/128], int32 sum8[K/8]
+ *     with sum8 = -8 * (sum of the 8 q8 values it covers),
+ *   - `stream` is a hipStream_t (NULL = the null stream).
+ * Every call is asynchronous on `stream`, allocates nothing, never
+ * synchronizes, and is safe under HIP graph capture.  `residual` may alias
+ * the output.  A NULL optional pointer means "skip", as in the reference.
+ *
+ * Return value: QE_OK, or a QE_ERR_* code; qe_last_error() then describes
+ * the failure (thread-local).  The C++ mirror in kernels.hpp turns a
+ * non-zero status into std::runtime_error, as the reference's
+ * CUDA_KERNEL_CHECK does (include/tensor.cuh:11-23).
+ */
+#ifndef QE_KERNELS_H
+#define QE_KERNELS_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QE_OK 0
+#define QE_ERR_INVALID_ARGUMENT 1 /* shape / alignment precondition violated */
+#define QE_ERR_UNSUPPORTED 2      /* shape outside what this build implements */
+#define QE_ERR_HIP 3              /* HIP runtime error at launch */
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char* qe_last_error(void);
+/* Library version string. */
+const char* qe_version(void);
+
+/* Device control block, same layout as the reference's DeviceControlBlock
+ * (include/tensor.cuh:28-34). */
+typedef struct __attribute__((aligned(256))) qe_device_control_block {
+    int32_t token_id;
+    int32_t seq_pos;
+    float temperature;
+    uint32_t reserved;
+    uint64_t rng_seed;
+} qe_device_control_block;
+
+/* Fused-QKV descriptor, same layout as QKVProjectionView
+ * (include/kernels.cuh:23-27). */
+typedef struct qe_qkv_view {
+    const void* q_weight; const uint16_t* q_scale; uint16_t* d_q;
+    const void* k_weight; const uint16_t* k_scale; uint16_t* d_k;
+    const void* v_weight; const uint16_t* v_scale; uint16_t* d_v;
+} qe_qkv_view;
+
+/* ---- Q8_1 quantizers ---------------------------------------------------- */
+
+/* Replaces launch_quantize_fp16_to_q8_1, include/kernels.cuh:50-57.
+ * fp16[num_elements] -> Q8_1.  num_elements % 128 == 0, input 16-byte aligned. */
+int qe_launch_quantize_fp16_to_q8_1(const uint16_t* input_x, int8_t* out_q8, float* out_scale,
+                                    int32_t* out_sum8, int num_elements, hipStream_t stream);
+
+/* Replaces launch_rmsnorm_q8_1, include/kernels.cuh:39-48.  One token:
+ * fp16 RMSNorm (optionally written to output_fp16_opt) then Q8_1 of the
+ * fp16-rounded normalized vector.  hidden_size % 128 == 0. */
+int qe_launch_rmsnorm_q8_1(const uint16_t* input, const uint16_t* gamma, uint16_t* output_fp16_opt,
+                           int8_t* out_q8, float* out_scale, int32_t* out_sum8,
+                           hipStream_t stream, int hidden_size);
+
+/* Replaces launch_rmsnorm_fp16, include/kernels.cuh:30-37 (prefill rows). */
+int qe_launch_rmsnorm_fp16(const uint16_t* input, const uint16_t* gamma, uint16_t* output,
+                           int num_tokens, hipStream_t stream, int hidden_size);
+
+/* ---- decode GEMV (W4A8: Q8_1 activations) -------------------------------- */
+
+/* Replaces launch_gemv_w4a8, include/kernels.cuh:71-82.
+ * y[n] = fp16( sum_g dot_g(n) * (s[n,g]*x_scale[g]) [+ residual[n]] ). */
+int qe_launch_gemv_w4a8(const uint32_t* qweight, const uint16_t* scales, const int8_t* input_q8,
+                        const float* input_scale, const int32_t* input_sum8, const uint16_t* residual,
+                        uint16_t* output_y, int out_features, int in_features, hipStream_t stream);
+
+/* Replaces launch_gemv_qkv_w4a8, include/kernels.cuh:84-94.  Rows
+ * [0,q_dim) -> d_q, [q_dim,q_dim+kv_dim) -> d_k, rest -> d_v. */
+int qe_launch_gemv_qkv_w4a8(const qe_qkv_view* view, const int8_t* input_q8, const float* input_scale,
+                            const int32_t* input_sum8, hipStream_t stream, int in_features,
+                            int num_q_heads, int num_kv_heads, int head_dim);
+
+/* Replaces launch_gemv_dual_gate_up_swiglu_w4a8, include/kernels.cuh:106-116.
+ * Weight rows are interleaved (2i = gate_i, 2i+1 = up_i);
+ * out[i] = fp16(silu(gate_i) * up_i). */
+int qe_launch_gemv_dual_gate_up_swiglu_w4a8(const uint32_t* gate_up_qweight, const uint16_t* gate_up_scales,
+                                            const int8_t* input_q8, const float* input_scale,
+                                            const int32_t* input_sum8, uint16_t* output_mlp,
+                                            int hidden_size, int intermediate_size, hipStream_t stream);
+
+/* ---- decode GEMV (W4A16: fp16 activations, quantized inside the launch) -- */
+
+/* Replaces launch_gemv_w4a16, include/kernels.cuh:60-69. */
+int qe_launch_gemv_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* input_x,
+                         const uint16_t* residual, uint16_t* output_y, int out_features, int in_features,
+                         hipStream_t stream);
+
+/* Replaces launch_gemv_dual_gate_up_swiglu_w4a16, include/kernels.cuh:96-104. */
+int qe_launch_gemv_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_qweight, const uint16_t* gate_up_scales,
+                                             const uint16_t* input_x, uint16_t* output_mlp,
+                                             int hidden_size, int intermediate_size, hipStream_t stream);
+
+/* ---- prefill dequant-GEMM (MFMA) ----------------------------------------- */
+
+/* Replaces launch_gemm_prefill_w4a16, include/kernels.cuh:119-130.
+ * Y[M,N] = fp16(A[M,K] . dequant(W)[N,K]^T), fp32 accumulation;
+ * residual added as fp16(fp16(acc) + residual).  `sm_count` is accepted for
+ * signature parity; tile selection uses the device's CU count. */
+int qe_launch_gemm_prefill_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* input_x,
+                                 const uint16_t* residual, uint16_t* output_y, int M, int N, int K,
+                                 hipStream_t stream, int sm_count);
+
+/* Replaces launch_gemm_prefill_qkv_w4a16, include/kernels.cuh:132-142. */
+int qe_launch_gemm_prefill_qkv_w4a16(const qe_qkv_view* view, const uint16_t* input_x, int M,
+                                     hipStream_t stream, int in_features, int num_q_heads,
+                                     int num_kv_heads, int head_dim, int sm_count);
+
+/* Replaces launch_gemm_prefill_dual_gate_up_swiglu_w4a16, include/kernels.cuh:144-153. */
+int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_qweight,
+                                                     const uint16_t* gate_up_scales, const uint16_t* input_x,
+                                                     uint16_t* output_mlp, int M, hipStream_t stream,
+                                                     int hidden_size, int intermediate_size);
+
+/* ---- greedy sampling ------------------------------------------------------ */
+
+/* Replaces launch_sample_and_advance, include/kernels.cuh:209-217, for
+ * greedy decoding (temperature <= 1e-5): argmax with the lowest index on
+ * ties, then token_id/seq_pos/rng_seed advance as the reference does.
+ * sample_scratch_val/idx hold >= 256 entries.  A control block with
+ * temperature > 1e-5 is rejected when it can be seen from the host
+ * (it lives in device memory, so the kernel itself falls back to greedy). */
+int qe_launch_sample_and_advance(const uint16_t* logits, float* sample_scratch_val,
+                                 int32_t* sample_scratch_idx, qe_device_control_block* d_control,
+                                 int32_t* d_mapped_pinned_token, hipStream_t stream, int vocab_size);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,127 @@
+// quant_primitives.hpp — gfx950 device primitives of the W4A16 G128 path.
+//
+// Same names and meaning as the reference's include/quant_primitives.cuh,
+// written for CDNA4: v_dot4_i32_i8 (sdot4) instead of __dp4a, DPP row
+// operations instead of warp shuffles, wave64 lanes.  HIP device code only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qwen {
+
+// ---- cross-lane helpers (DPP within a 16-lane row, ds_swizzle across 32) --
+// DPP controls (GFX9 encoding): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,
+// row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+// ds_swizzle bit-mode: and_mask=0x1F, xor_mask=0x10 -> lane ^ 16 within 32 lanes.
+__device__ __forceinline__ float swz_xor16_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+
+// All-reduce (sum) over aligned groups of SEG lanes; every lane of the group
+// ends with the total.  SEG in {1,2,4,8,16,32,64}.
+template <int SEG>
+__device__ __forceinline__ float seg_sum(float v) {
+    if constexpr (SEG >= 2) v += dpp_f32<0xB1>(v);
+    if constexpr (SEG >= 4) v += dpp_f32<0x4E>(v);
+    if constexpr (SEG >= 8) v += dpp_f32<0x141>(v);
+    if constexpr (SEG >= 16) v += dpp_f32<0x140>(v);
+    if constexpr (SEG >= 32) v += swz_xor16_f32(v);
+    if constexpr (SEG >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+template <int SEG>
+__device__ __forceinline__ float seg_max(float v) {
+    if constexpr (SEG >= 2) v = fmaxf(v, dpp_f32<0xB1>(v));
+    if constexpr (SEG >= 4) v = fmaxf(v, dpp_f32<0x4E>(v));
+    if constexpr (SEG >= 8) v = fmaxf(v, dpp_f32<0x141>(v));
+    if constexpr (SEG >= 16) v = fmaxf(v, dpp_f32<0x140>(v));
+    if constexpr (SEG >= 32) v = fmaxf(v, swz_xor16_f32(v));
+    if constexpr (SEG >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+
+// ---- integer dot primitives ---------------------------------------------
+// compute_q8_sum8 (reference quant_primitives.cuh:13-17): -8 * sum of the
+// 8 signed bytes of (x_lo, x_hi).
+__device__ __forceinline__ int32_t compute_q8_sum8(int32_t x_lo, int32_t x_hi) {
+    int32_t s = __builtin_amdgcn_sdot4(0x01010101, x_hi, 0, false);
+    s = __builtin_amdgcn_sdot4(0x01010101, x_lo, s, false);
+    return -8 * s;
+}
+
+// dp4a_w4_q8_oct (reference quant_primitives.cuh:28-32): sum_j (q_j-8)*x_j
+// over one packed word = sdot4(w_hi, x_hi, sdot4(w_lo, x_lo, sum8)).
+// Nibbles are 0..15, so they are valid signed int8 lanes of sdot4.
+__device__ __forceinline__ int32_t dp4a_w4_q8_oct(uint32_t packed, int32_t x_lo, int32_t x_hi, int32_t x_sum8) {
+    int32_t w_lo = static_cast<int32_t>(packed & 0x0F0F0F0Fu);
+    int32_t w_hi = static_cast<int32_t>((packed >> 4) & 0x0F0F0F0Fu);
+    return __builtin_amdgcn_sdot4(w_hi, x_hi, __builtin_amdgcn_sdot4(w_lo, x_lo, x_sum8, false), false);
+}
+
+// ---- Q8_1 quantization of one 128-element group --------------------------
+// 16 consecutive lanes hold 8 values each (lane l: elements 8l..8l+7).
+// d = max(max|x|/127, 1e-8) (IEEE division), inv_d = 1/d (IEEE),
+// q = clamp(roundf(x*inv_d), +-127) with roundf = half away from zero, as the
+// reference CPU golden (tests/test_kernels.cu:311-326).  The caller's 16-lane
+// group must be a DPP row (lane index multiple of 16).
+struct Q8Group {
+    int32_t x_lo, x_hi;  // packed q8 of the lane's 8 elements
+    int32_t sum8;        // -8 * sum of those 8 values
+    float d;             // group scale (same in all 16 lanes)
+};
+
+__device__ __forceinline__ Q8Group quantize_group128_q8_1(const float vals[8]) {
+    float max_abs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) max_abs = fmaxf(max_abs, fabsf(vals[j]));
+    max_abs = seg_max<16>(max_abs);
+    float d = fmaxf(max_abs / 127.0f, 1e-8f);
+    float inv_d = 1.0f / d;
+    uint32_t b[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        int v = static_cast<int>(roundf(vals[j] * inv_d));
+        v = max(-127, min(127, v));
+        b[j] = static_cast<uint32_t>(v) & 0xFFu;
+    }
+    Q8Group g;
+    g.x_lo = static_cast<int32_t>(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24));
+    g.x_hi = static_cast<int32_t>(b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+    g.sum8 = compute_q8_sum8(g.x_lo, g.x_hi);
+    g.d = d;
+    return g;
+}
+
+// ---- int4 -> fp16 dequantization -------------------------------------------
+// unpack_w4_to_half2_quad (reference quant_primitives.cuh:92-115): the 8
+// elements of a packed word in K order, (q-8)*scale with one fp16 RNE
+// multiply.  (q-8) is formed exactly with the 0x6400 (1024.0) bias.
+typedef _Float16 qe_half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 qe_half8_t __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ qe_half8_t unpack_w4_to_half8(uint32_t packed, _Float16 scale) {
+    const uint32_t bias1024 = 0x64006400u;
+    uint32_t u01 = (packed & 0x000Fu) | ((packed & 0x0F00u) << 8) | bias1024;
+    uint32_t u23 = ((packed >> 16) & 0x000Fu) | ((packed >> 8) & 0x000F0000u) | bias1024;
+    uint32_t u45 = ((packed >> 4) & 0x000Fu) | ((packed << 4) & 0x000F0000u) | bias1024;
+    uint32_t u67 = ((packed >> 20) & 0x000Fu) | ((packed >> 12) & 0x000F0000u) | bias1024;
+    const qe_half2_t b = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const qe_half2_t s = {scale, scale};
+    qe_half2_t h01 = (__builtin_bit_cast(qe_half2_t, u01) - b) * s;
+    qe_half2_t h23 = (__builtin_bit_cast(qe_half2_t, u23) - b) * s;
+    qe_half2_t h45 = (__builtin_bit_cast(qe_half2_t, u45) - b) * s;
+    qe_half2_t h67 = (__builtin_bit_cast(qe_half2_t, u67) - b) * s;
+    return qe_half8_t{h01[0], h01[1], h23[0], h23[1], h45[0], h45[1], h67[0], h67[1]};
+}
+
+}  // namespace qwen

@@ -1,0 +1,54 @@
+// Shared host/device helpers of libqe_amd: status reporting, device facts,
+// fp16 conversions.  gfx950 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "qe_kernels.h"
+#include "quant_primitives.hpp"
+
+namespace qe {
+
+// Native 128-bit vector (usable with __builtin_nontemporal_load).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Thread-local text of the last failure, returned by qe_last_error().
+void set_error(const char* fmt, ...);
+void clear_error();
+
+// Number of compute units of the current device (cached per device).
+int cu_count();
+
+inline int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    set_error("%s", buf);
+    return code;
+}
+
+// Checked at the end of every entry point, like CUDA_KERNEL_CHECK in the
+// reference (include/tensor.cuh:23).
+inline int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(QE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    clear_error();
+    return QE_OK;
+}
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+__device__ __forceinline__ float h2f(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+
+}  // namespace qe
+
+#define QE_REQUIRE(cond, ...)                                              \
+    do {                                                                   \
+        if (!(cond)) return ::qe::fail(QE_ERR_INVALID_ARGUMENT, __VA_ARGS__); \
+    } while (0)

@@ -1,0 +1,40 @@
+// Host-side runtime helpers of libqe_amd: thread-local error text, version,
+// cached device facts.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "qe_common.hpp"
+
+namespace qe {
+
+namespace {
+thread_local char g_last_error[1024] = "";
+int g_cu_count[64] = {0};
+}  // namespace
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+}
+
+void clear_error() { g_last_error[0] = '\0'; }
+
+int cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (g_cu_count[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        g_cu_count[dev] = n;
+    }
+    return g_cu_count[dev];
+}
+
+}  // namespace qe
+
+extern "C" const char* qe_last_error(void) { return qe::g_last_error; }
+
+extern "C" const char* qe_version(void) { return "qe_amd 0.1 (gfx950)"; }

@@ -1,0 +1,169 @@
+"""Python binding of libqe_amd.so (the C-ABI in include/qe_kernels.h).
+
+The library is the product: this module only loads it with ctypes and
+passes device pointers of torch tensors (torch provides HBM allocations and
+streams).  There is no fallback: if the library is missing, `lib()` raises.
+
+Function names mirror the reference's launchers (include/kernels.cuh) with
+the same argument order; a non-zero status raises RuntimeError carrying
+qe_last_error(), as the reference's CUDA_KERNEL_CHECK throws
+std::runtime_error (include/tensor.cuh:11-23).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqe_amd.so")
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+
+# (name, argtypes) of every entry point declared in include/qe_kernels.h
+SIGNATURES = {
+    "qe_launch_quantize_fp16_to_q8_1": [_P, _P, _P, _P, _I, _P],
+    "qe_launch_rmsnorm_q8_1": [_P, _P, _P, _P, _P, _P, _P, _I],
+    "qe_launch_rmsnorm_fp16": [_P, _P, _P, _I, _P, _I],
+    "qe_launch_gemv_w4a8": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _P],
+    "qe_launch_gemv_qkv_w4a8": [_P, _P, _P, _P, _P, _I, _I, _I, _I],
+    "qe_launch_gemv_dual_gate_up_swiglu_w4a8": [_P, _P, _P, _P, _P, _P, _I, _I, _P],
+    "qe_launch_gemv_w4a16": [_P, _P, _P, _P, _P, _I, _I, _P],
+    "qe_launch_gemv_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _I, _I, _P],
+    "qe_launch_gemm_prefill_w4a16": [_P, _P, _P, _P, _P, _I, _I, _I, _P, _I],
+    "qe_launch_gemm_prefill_qkv_w4a16": [_P, _P, _I, _P, _I, _I, _I, _I, _I],
+    "qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _I, _P, _I, _I],
+    "qe_launch_sample_and_advance": [_P, _P, _P, _P, _P, _P, _I],
+}
+
+_lib = None
+
+
+class QKVView(ctypes.Structure):
+    """qe_qkv_view / QKVProjectionView (include/kernels.cuh:23-27)."""
+    _fields_ = [(n, _P) for n in ("q_weight", "q_scale", "d_q", "k_weight", "k_scale", "d_k",
+                                   "v_weight", "v_scale", "d_v")]
+
+
+def build(jobs: int = 8) -> str:
+    """Compile libqe_amd.so in-tree for gfx950 (hipcc; no GPU needed)."""
+    subprocess.run(["make", "-s", "-C", _HERE, f"-j{jobs}"], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libqe_amd.so not built at {LIB_PATH}; run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        L.qe_last_error.restype = ctypes.c_char_p
+        L.qe_version.restype = ctypes.c_char_p
+        _lib = L
+    return _lib
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _check(rc: int, name: str):
+    if rc != 0:
+        msg = lib().qe_last_error().decode()
+        raise RuntimeError(f"{name} failed (status {rc}): {msg}")
+
+
+def _call(name, *args):
+    _check(getattr(lib(), name)(*args), name)
+
+
+# ---- launchers (reference names, tensor arguments) ---------------------------
+def launch_quantize_fp16_to_q8_1(input_x, out_q8, out_scale, out_sum8, num_elements, stream=None):
+    _call("qe_launch_quantize_fp16_to_q8_1", _ptr(input_x), _ptr(out_q8), _ptr(out_scale), _ptr(out_sum8),
+          num_elements, _stream(stream))
+
+
+def launch_rmsnorm_q8_1(input, gamma, output_fp16_opt, out_q8, out_scale, out_sum8, stream=None,
+                        hidden_size=1536):
+    _call("qe_launch_rmsnorm_q8_1", _ptr(input), _ptr(gamma), _ptr(output_fp16_opt), _ptr(out_q8),
+          _ptr(out_scale), _ptr(out_sum8), _stream(stream), hidden_size)
+
+
+def launch_rmsnorm_fp16(input, gamma, output, num_tokens, stream=None, hidden_size=1536):
+    _call("qe_launch_rmsnorm_fp16", _ptr(input), _ptr(gamma), _ptr(output), num_tokens, _stream(stream),
+          hidden_size)
+
+
+def launch_gemv_w4a8(qweight, scales, input_q8, input_scale, input_sum8, residual, output_y,
+                     out_features, in_features, stream=None):
+    _call("qe_launch_gemv_w4a8", _ptr(qweight), _ptr(scales), _ptr(input_q8), _ptr(input_scale),
+          _ptr(input_sum8), _ptr(residual), _ptr(output_y), out_features, in_features, _stream(stream))
+
+
+def make_qkv_view(q_weight, q_scale, d_q, k_weight, k_scale, d_k, v_weight, v_scale, d_v) -> QKVView:
+    return QKVView(*[_ptr(t) for t in (q_weight, q_scale, d_q, k_weight, k_scale, d_k, v_weight, v_scale, d_v)])
+
+
+def launch_gemv_qkv_w4a8(view: QKVView, input_q8, input_scale, input_sum8, stream=None, in_features=1536,
+                         num_q_heads=12, num_kv_heads=2, head_dim=128):
+    _call("qe_launch_gemv_qkv_w4a8", ctypes.addressof(view), _ptr(input_q8), _ptr(input_scale),
+          _ptr(input_sum8), _stream(stream), in_features, num_q_heads, num_kv_heads, head_dim)
+
+
+def launch_gemv_dual_gate_up_swiglu_w4a8(gate_up_qweight, gate_up_scales, input_q8, input_scale, input_sum8,
+                                         output_mlp, hidden_size, intermediate_size, stream=None):
+    _call("qe_launch_gemv_dual_gate_up_swiglu_w4a8", _ptr(gate_up_qweight), _ptr(gate_up_scales),
+          _ptr(input_q8), _ptr(input_scale), _ptr(input_sum8), _ptr(output_mlp), hidden_size,
+          intermediate_size, _stream(stream))
+
+
+def launch_gemv_w4a16(qweight, scales, input_x, residual, output_y, out_features, in_features, stream=None):
+    _call("qe_launch_gemv_w4a16", _ptr(qweight), _ptr(scales), _ptr(input_x), _ptr(residual), _ptr(output_y),
+          out_features, in_features, _stream(stream))
+
+
+def launch_gemv_dual_gate_up_swiglu_w4a16(gate_up_qweight, gate_up_scales, input_x, output_mlp, hidden_size,
+                                          intermediate_size, stream=None):
+    _call("qe_launch_gemv_dual_gate_up_swiglu_w4a16", _ptr(gate_up_qweight), _ptr(gate_up_scales),
+          _ptr(input_x), _ptr(output_mlp), hidden_size, intermediate_size, _stream(stream))
+
+
+def launch_gemm_prefill_w4a16(qweight, scales, input_x, residual, output_y, M, N, K, stream=None, sm_count=0):
+    _call("qe_launch_gemm_prefill_w4a16", _ptr(qweight), _ptr(scales), _ptr(input_x), _ptr(residual),
+          _ptr(output_y), M, N, K, _stream(stream), sm_count)
+
+
+def launch_gemm_prefill_qkv_w4a16(view: QKVView, input_x, M, stream=None, in_features=1536, num_q_heads=12,
+                                  num_kv_heads=2, head_dim=128, sm_count=0):
+    _call("qe_launch_gemm_prefill_qkv_w4a16", ctypes.addressof(view), _ptr(input_x), M, _stream(stream),
+          in_features, num_q_heads, num_kv_heads, head_dim, sm_count)
+
+
+def launch_gemm_prefill_dual_gate_up_swiglu_w4a16(gate_up_qweight, gate_up_scales, input_x, output_mlp, M,
+                                                  stream=None, hidden_size=1536, intermediate_size=8960):
+    _call("qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16", _ptr(gate_up_qweight), _ptr(gate_up_scales),
+          _ptr(input_x), _ptr(output_mlp), M, _stream(stream), hidden_size, intermediate_size)
+
+
+def launch_sample_and_advance(logits, sample_scratch_val, sample_scratch_idx, d_control, d_mapped_pinned_token,
+                              stream=None, vocab_size=151936):
+    _call("qe_launch_sample_and_advance", _ptr(logits), _ptr(sample_scratch_val), _ptr(sample_scratch_idx),
+          _ptr(d_control), _ptr(d_mapped_pinned_token), _stream(stream), vocab_size)

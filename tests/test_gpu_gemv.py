@@ -1,0 +1,162 @@
+"""GPU parity of the decode GEMV family against the CPU oracle.
+
+Reference: src/kernels/gemv_w4a16.cu (launchers :864-999), CPU golden
+tests/test_kernels.cu:308-363.  Integer stage: the oracle's per-group dots
+are exact; the fp16 outputs are compared with the tolerance of
+helpers.assert_fp16_close (2 fp16 ulp / 1e-3 relative).
+Shapes: BASELINE configs[0] (W4A16 1536->8960), configs[1] (QKV, O, gate+up
+SwiGLU, down), configs[2] (LM head + argmax) and the reference's Suite 3
+dimension sweep (test_kernels.cu:251-256).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_fp16_close, dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def qe():
+    import qe_amd
+    qe_amd.lib()
+    return qe_amd
+
+
+def _act(orc, K, seed):
+    x = orc.synth_f16_normal(seed, K)
+    q8, xs, s8 = orc.quantize_q8_1(x)
+    return x, q8, xs, s8
+
+
+def _gemv_w4a8(qe, qw, sc, q8, xs, s8, N, K, residual=None, inplace=False):
+    out = dev(residual) if inplace else empty(N, torch.float16)
+    res = out if inplace else (dev(residual) if residual is not None else None)
+    qe.launch_gemv_w4a8(dev(qw), dev(sc), dev(q8), dev(xs), dev(s8), res, out, N, K)
+    return host(out)
+
+
+@pytest.mark.parametrize("N,K", [(1536, 1536), (1536, 8960), (8960, 1536), (64, 256), (1, 128), (37, 384),
+                                 (1000, 2560), (300, 16384), (130, 16512), (77, 32768)])
+def test_gemv_w4a8_shapes(qe, orc, N, K):
+    print(f"gemv_w4a8 N={N} K={K}", flush=True)
+    qw, sc = orc.synth_w4(N * 7 + K, N, K)
+    _, q8, xs, s8 = _act(orc, K, K)
+    got = _gemv_w4a8(qe, qw, sc, q8, xs, s8, N, K)
+    ref, ex, bd = orc.gemv_w4a8(qw, sc, q8, xs, s8, N, K)
+    assert_fp16_close(got, ex, bd, ref, what=f"gemv {N}x{K}")
+
+
+@pytest.mark.parametrize("N,K", [(1536, 1536), (1536, 8960)])
+def test_gemv_w4a8_residual_inplace(qe, orc, N, K):
+    """O-proj / down-proj of the decode layer: residual == output
+    (src/engine.cu:396-400, :426-430)."""
+    qw, sc = orc.synth_w4(5 + K, N, K)
+    _, q8, xs, s8 = _act(orc, K, 3)
+    res = orc.synth_f16_normal(11, N)
+    got = _gemv_w4a8(qe, qw, sc, q8, xs, s8, N, K, residual=res, inplace=True)
+    ref, ex, bd = orc.gemv_w4a8(qw, sc, q8, xs, s8, N, K, residual=res)
+    assert_fp16_close(got, ex, bd, ref, what="residual in place")
+    got2 = _gemv_w4a8(qe, qw, sc, q8, xs, s8, N, K, residual=res, inplace=False)
+    assert np.array_equal(got2, got)
+
+
+def test_gemv_uses_given_sum8(qe, orc):
+    """sum8 is the dp4a seed (quant_primitives.cuh:28-32): a perturbed sum8
+    changes the result exactly as in the oracle."""
+    N, K = 256, 1536
+    qw, sc = orc.synth_w4(1, N, K)
+    _, q8, xs, s8 = _act(orc, K, 2)
+    s8 = s8.copy()
+    s8[::7] += 40
+    got = _gemv_w4a8(qe, qw, sc, q8, xs, s8, N, K)
+    ref, ex, bd = orc.gemv_w4a8(qw, sc, q8, xs, s8, N, K)
+    assert_fp16_close(got, ex, bd, ref, what="perturbed sum8")
+
+
+def test_gemv_unaligned_weights_take_generic_path(qe, orc):
+    N, K = 200, 1536
+    qw, sc = orc.synth_w4(21, N, K)
+    _, q8, xs, s8 = _act(orc, K, 4)
+    buf = dev(np.concatenate([np.zeros(1, np.uint32), qw.reshape(-1)]))
+    w_ptr = buf.data_ptr() + 4  # 4-byte aligned, not 16-byte aligned
+    out = empty(N, torch.float16)
+    qe.launch_gemv_w4a8(w_ptr, dev(sc), dev(q8), dev(xs), dev(s8), None, out, N, K)
+    ref, ex, bd = orc.gemv_w4a8(qw, sc, q8, xs, s8, N, K)
+    assert_fp16_close(host(out), ex, bd, ref, what="unaligned")
+
+
+def test_gemv_qkv(qe, orc):
+    K, nq, nkv, hd = 1536, 12, 2, 128
+    mats = [orc.synth_w4(100 + i, n, K) for i, n in enumerate((nq * hd, nkv * hd, nkv * hd))]
+    _, q8, xs, s8 = _act(orc, K, 8)
+    outs = [empty(n, torch.float16) for n in (nq * hd, nkv * hd, nkv * hd)]
+    dw = [(dev(w), dev(s)) for w, s in mats]
+    view = qe.make_qkv_view(dw[0][0], dw[0][1], outs[0], dw[1][0], dw[1][1], outs[1], dw[2][0], dw[2][1], outs[2])
+    qe.launch_gemv_qkv_w4a8(view, dev(q8), dev(xs), dev(s8), in_features=K, num_q_heads=nq, num_kv_heads=nkv,
+                            head_dim=hd)
+    for (w, s), o, n in zip(mats, outs, (nq * hd, nkv * hd, nkv * hd)):
+        ref, ex, bd = orc.gemv_w4a8(w, s, q8, xs, s8, n, K)
+        assert_fp16_close(host(o), ex, bd, ref, what="qkv")
+
+
+@pytest.mark.parametrize("I,K", [(8960, 1536), (512, 256), (1536, 8960)])
+def test_gemv_swiglu_w4a8(qe, orc, I, K):
+    qw, sc = orc.synth_w4(33 + I, 2 * I, K)
+    _, q8, xs, s8 = _act(orc, K, 9)
+    out = empty(I, torch.float16)
+    qe.launch_gemv_dual_gate_up_swiglu_w4a8(dev(qw), dev(sc), dev(q8), dev(xs), dev(s8), out, K, I)
+    ref, ex, bd = orc.gemv_swiglu_w4a8(qw, sc, q8, xs, s8, K, I)
+    assert_fp16_close(host(out), ex, bd, ref, what="swiglu w4a8")
+
+
+@pytest.mark.parametrize("N,K", [(8960, 1536), (1536, 8960), (64, 128), (333, 2560), (50, 20480)])
+def test_gemv_w4a16(qe, orc, N, K):
+    """W4A16 GEMV 1536->8960 with in-launch Q8_1 quantization."""
+    print(f"gemv_w4a16 N={N} K={K}", flush=True)
+    qw, sc = orc.synth_w4(77 + N, N, K)
+    x = orc.synth_f16_normal(K + 1, K)
+    res = orc.synth_f16_normal(K + 2, N)
+    out = empty(N, torch.float16)
+    qe.launch_gemv_w4a16(dev(qw), dev(sc), dev(x), dev(res), out, N, K)
+    ref, ex, bd = orc.gemv_w4a16(qw, sc, x, N, K, residual=res)
+    assert_fp16_close(host(out), ex, bd, ref, what="w4a16")
+
+
+@pytest.mark.parametrize("H,I", [(1536, 8960), (2560, 10240), (5120, 27648), (256, 512)])
+def test_suite3_swiglu_w4a16_sweep(qe, orc, H, I):
+    """The reference's Synthetic Suite 3 (tests/test_kernels.cu:242-403):
+    same generator, same entry point, its max|err| <= 5e-3 bar, and the
+    oracle tolerance on top."""
+    print(f"suite3 H={H} I={I}", flush=True)
+    x, qw, sc = orc.suite3_inputs(H, I)
+    out = empty(I, torch.float16)
+    qe.launch_gemv_dual_gate_up_swiglu_w4a16(dev(qw), dev(sc), dev(x), out, H, I)
+    got = host(out)
+    ref, ex, bd = orc.gemv_swiglu_w4a16(qw, sc, x, H, I)
+    assert np.abs(got.astype(np.float32) - ref.astype(np.float32)).max() <= 5e-3
+    assert_fp16_close(got, ex, bd, ref, what="suite3")
+
+
+def test_lm_head_and_argmax(qe, orc):
+    """LM head 1536 -> 151936 then greedy argmax (bit-exact)."""
+    N, K = 151936, 1536
+    qw, sc = orc.synth_w4(2024, N, K)
+    _, q8, xs, s8 = _act(orc, K, 12)
+    logits = empty(N, torch.float16)
+    qe.launch_gemv_w4a8(dev(qw), dev(sc), dev(q8), dev(xs), dev(s8), None, logits, N, K)
+    got = host(logits)
+    ref, ex, bd = orc.gemv_w4a8(qw, sc, q8, xs, s8, N, K)
+    assert_fp16_close(got, ex, bd, ref, what="lm head")
+    val = empty(256, torch.float32)
+    idx = empty(256, torch.int32)
+    tok = empty(1, torch.int32)
+    qe.launch_sample_and_advance(logits, val, idx, None, tok, vocab_size=N)
+    assert int(host(tok)[0]) == orc.argmax_f16(got)
+
+
+def test_gemv_rejects_bad_k(qe):
+    with pytest.raises(RuntimeError, match="multiple of 128"):
+        qe.launch_gemv_w4a8(empty(10, torch.int32), empty(10, torch.float16), empty(100, torch.int8),
+                            empty(1, torch.float32), empty(13, torch.int32), None, empty(4, torch.float16), 4, 100)
