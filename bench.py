@@ -1,0 +1,298 @@
+#!/usr/bin/env python3
+"""Benchmark of the W4A16 G128 matrix path on one MI355X.
+
+Headline (BASELINE.json metric "W4A16 GEMV GB/s (% HBM peak)"), workload
+one step = the per-token decode projection set of one
+Qwen2.5-1.5B layer, as src/engine.cu:361-431 issues it:
+    rmsnorm_q8_1 -> QKV GEMV (1536->2048) -> O GEMV (1536->1536, +residual)
+    -> rmsnorm_q8_1 -> gate+up SwiGLU GEMV (1536->2x8960) -> quantize(8960)
+    -> down GEMV (8960->1536, +residual)
+value = algorithmic GEMV bytes per step / step time.  Every step uses
+another copy of the layer's weights; the copies span >= 512 MB (twice the
+256 MB Infinity Cache) so the weights stream from HBM.  Steps are replayed
+from one HIP graph (the reference decodes from a CUDA graph, engine.cu:453-470).
+
+Also reported: per-kernel GB/s and roofline of the dominant kernel (gate+up),
+configs[0] (W4A16 GEMV 1536->8960), configs[2] (LM head + argmax),
+configs[3] (prefill dequant-GEMM TFLOP/s), and the oracle CPU baseline.
+Inputs are synthetic (seeded), weights random in the packed layout.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qwen-engine_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+H, I, V, NQ, NKV, HD = 1536, 8960, 151936, 12, 2, 128
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+POOL_BYTES = 512 << 20
+
+
+def gemv_bytes(N, K, act="q8", out_n=None):
+    """Algorithmic bytes of one GEMV: packed weights + fp16 scales + activation + output."""
+    a = K * 2 if act == "f16" else K + K // 32 + K // 2
+    return N * K // 2 + N * (K // 128) * 2 + a + (out_n if out_n is not None else N) * 2
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only-step", action="store_true", help="headline step only (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (the W4A16 path has no multi-GPU "
+              "component; see DESIGN.md for how it would shard). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import qe_amd
+
+    qe_amd.lib()
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+
+    def rand_w4(N, K, copies):
+        qw = torch.randint(-2 ** 31, 2 ** 31 - 1, (copies, N, K // 8), dtype=torch.int32, device=dev, generator=gen)
+        sc = (torch.randn((copies, N, K // 128), device=dev, generator=gen).abs() * 0.02).half()
+        return qw, sc
+
+    def copies_for(nbytes):
+        return max(2, -(-POOL_BYTES // nbytes))
+
+    def graph_of(fn, reps):
+        """Capture fn(i) for i in range(reps) into one graph."""
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(min(reps, 3)):
+                fn(i)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(reps):
+                fn(i)
+        return g
+
+    def time_graph(g, replays):
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / replays  # ms per graph
+
+    # ---------------- activations / scratch ----------------------------------
+    x = torch.randn(H, device=dev, generator=gen).half()
+    hidden = x.clone()
+    gamma = torch.ones(H, device=dev, dtype=torch.float16)
+    q8 = torch.empty(I, dtype=torch.int8, device=dev)
+    xs = torch.empty(I // 128, dtype=torch.float32, device=dev)
+    s8 = torch.empty(I // 8, dtype=torch.int32, device=dev)
+    dq = torch.empty(NQ * HD, dtype=torch.float16, device=dev)
+    dk = torch.empty(NKV * HD, dtype=torch.float16, device=dev)
+    dv = torch.empty(NKV * HD, dtype=torch.float16, device=dev)
+    mlp = torch.empty(I, dtype=torch.float16, device=dev)
+
+    # ---------------- headline: per-layer decode projection set --------------
+    b_qkv = gemv_bytes(NQ * HD + 2 * NKV * HD, H)
+    b_o = gemv_bytes(H, H) + H * 2          # + fp16 residual read
+    b_gu = gemv_bytes(2 * I, H, out_n=I)
+    b_down = gemv_bytes(H, I) + H * 2
+    step_bytes = b_qkv + b_o + b_gu + b_down
+    L = copies_for(step_bytes)
+    wq, sq = rand_w4(NQ * HD, H, L)
+    wk, sk = rand_w4(NKV * HD, H, L)
+    wv, sv = rand_w4(NKV * HD, H, L)
+    wo, so = rand_w4(H, H, L)
+    wgu, sgu = rand_w4(2 * I, H, L)
+    wd, sd = rand_w4(H, I, L)
+    views = [qe_amd.make_qkv_view(wq[l], sq[l], dq, wk[l], sk[l], dk, wv[l], sv[l], dv) for l in range(L)]
+
+    def layer_step(i):
+        l = i % L
+        qe_amd.launch_rmsnorm_q8_1(hidden, gamma, None, q8, xs, s8, hidden_size=H)
+        qe_amd.launch_gemv_qkv_w4a8(views[l], q8, xs, s8, in_features=H, num_q_heads=NQ, num_kv_heads=NKV,
+                                    head_dim=HD)
+        # attention is outside this path: its Q8_1 output is stood in by the
+        # current activation (same shape, K = 1536)
+        qe_amd.launch_gemv_w4a8(wo[l], so[l], q8, xs, s8, hidden, hidden, H, H)
+        qe_amd.launch_rmsnorm_q8_1(hidden, gamma, None, q8, xs, s8, hidden_size=H)
+        qe_amd.launch_gemv_dual_gate_up_swiglu_w4a8(wgu[l], sgu[l], q8, xs, s8, mlp, H, I)
+        qe_amd.launch_quantize_fp16_to_q8_1(mlp, q8, xs, s8, I)
+        qe_amd.launch_gemv_w4a8(wd[l], sd[l], q8, xs, s8, hidden, hidden, H, I)
+
+    K_steps = max(args.steps, 1)
+    g_step = graph_of(layer_step, K_steps)
+    for _ in range(max(1, args.warmup // max(1, K_steps))):
+        g_step.replay()
+    torch.cuda.synchronize()
+    ms_graph = time_graph(g_step, 3)
+    ms_per_step = ms_graph / K_steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    result = {
+        "metric": "W4A16 GEMV GB/s (% HBM peak); decode tok/s Qwen2.5-1.5B tg256",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K_steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 x int4 -> int32 (sdot4), fp32 scale/accumulate, fp16 out",
+        "data": "synthetic (seeded random packed int4 weights, |N(0,1)|*0.02 fp16 scales, N(0,1) fp16 x)",
+        "config": {
+            "workload": "configs[1]: one Qwen2.5-1.5B layer decode projection set, batch 1 "
+                        "(QKV 1536->2048, O 1536->1536 +res, gate+up 1536->2x8960 SwiGLU, down 8960->1536 +res, "
+                        "with rmsnorm_q8_1 x2 and quantize(8960))",
+            "bytes_per_step": step_bytes,
+            "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+            "weight_copies": L,
+            "timing": "HIP graph of K steps, hipEvents, weights rotated over >= 512 MB",
+        },
+    }
+    if args.only_step:
+        print(json.dumps(result))
+        return
+
+    # ---------------- per-kernel GEMV roofline -------------------------------
+    def kernel_gbs(name, N, K, launch, nbytes, copies_bytes):
+        C = copies_for(copies_bytes)
+        qw, sc = rand_w4(N, K, C)
+        g = graph_of(lambda i: launch(qw[i % C], sc[i % C]), C)
+        ms = time_graph(g, 5) / C
+        return {"kernel": name, "us": round(ms * 1e3, 3), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+
+    per = []
+    qe_amd.launch_rmsnorm_q8_1(hidden, gamma, None, q8, xs, s8, hidden_size=H)
+    torch.cuda.synchronize()
+    per.append(kernel_gbs("gemv_w4a8 O 1536->1536", H, H,
+                          lambda w, s: qe_amd.launch_gemv_w4a8(w, s, q8, xs, s8, None, mlp, H, H),
+                          gemv_bytes(H, H), H * H // 2))
+    per.append(kernel_gbs("gemv_w4a8 QKV-shape 1536->2048", 2048, H,
+                          lambda w, s: qe_amd.launch_gemv_w4a8(w, s, q8, xs, s8, None, mlp, 2048, H),
+                          gemv_bytes(2048, H), 2048 * H // 2))
+    gu = kernel_gbs("gemv_dual_gate_up_swiglu_w4a8 1536->2x8960", 2 * I, H,
+                    lambda w, s: qe_amd.launch_gemv_dual_gate_up_swiglu_w4a8(w, s, q8, xs, s8, mlp, H, I),
+                    b_gu, 2 * I * H // 2)
+    per.append(gu)
+    qe_amd.launch_quantize_fp16_to_q8_1(mlp, q8, xs, s8, I)
+    torch.cuda.synchronize()
+    per.append(kernel_gbs("gemv_w4a8 down 8960->1536", H, I,
+                          lambda w, s: qe_amd.launch_gemv_w4a8(w, s, q8, xs, s8, None, hidden, H, I),
+                          gemv_bytes(H, I), H * I // 2))
+    qe_amd.launch_rmsnorm_q8_1(hidden, gamma, None, q8, xs, s8, hidden_size=H)
+    torch.cuda.synchronize()
+    logits = torch.empty(V, dtype=torch.float16, device=dev)
+    lm = kernel_gbs("gemv_w4a8 LM head 1536->151936", V, H,
+                    lambda w, s: qe_amd.launch_gemv_w4a8(w, s, q8, xs, s8, None, logits, V, H),
+                    gemv_bytes(V, H), V * H // 2)
+    per.append(lm)
+    c0 = kernel_gbs("gemv_w4a16 configs[0] 1536->8960", I, H,
+                    lambda w, s: qe_amd.launch_gemv_w4a16(w, s, x, None, mlp, I, H),
+                    gemv_bytes(I, H, act="f16"), I * H // 2)
+    per.append(c0)
+
+    result["roofline"] = {
+        "kernel": gu["kernel"],
+        "bound": "hbm",
+        "achieved": gu["GB/s"],
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": gu["frac"],
+        "traffic": None,
+        "bytes_per_launch": b_gu,
+        "avg_launch_us": gu["us"],
+    }
+    result["kernels"] = per
+
+    # ---------------- LM head + argmax ----------------------------
+    val = torch.empty(256, dtype=torch.float32, device=dev)
+    idx = torch.empty(256, dtype=torch.int32, device=dev)
+    tok = torch.empty(1, dtype=torch.int32, device=dev)
+    C = copies_for(V * H // 2)
+    wl, sl = rand_w4(V, H, C)
+
+    def lm_argmax(i):
+        qe_amd.launch_gemv_w4a8(wl[i % C], sl[i % C], q8, xs, s8, None, logits, V, H)
+        qe_amd.launch_sample_and_advance(logits, val, idx, None, tok, vocab_size=V)
+
+    ms = time_graph(graph_of(lm_argmax, C), 5) / C
+    result["lm_head_argmax"] = {"us": round(ms * 1e3, 3), "GB/s": round(gemv_bytes(V, H) / (ms * 1e-3) / 1e9, 1)}
+    del wl, sl
+
+    # ---------------- prefill dequant-GEMM -----------------------
+    pre = []
+    for M in (128, 512, 1024):
+        A = torch.randn((M, I), device=dev, generator=gen).half()
+        outp = torch.empty((M, 2 * I), dtype=torch.float16, device=dev)
+        tot_flop, tot_ms = 0.0, 0.0
+        for (N, K, name) in ((2048, H, "qkv"), (H, H, "o"), (2 * I, H, "gate_up"), (H, I, "down")):
+            C = max(2, min(64, copies_for(N * K // 2)))
+            qw, sc = rand_w4(N, K, C)
+            if name == "gate_up":
+                fn = lambda i: qe_amd.launch_gemm_prefill_dual_gate_up_swiglu_w4a16(
+                    qw[i % C], sc[i % C], A, outp, M, hidden_size=K, intermediate_size=I)
+            else:
+                fn = lambda i: qe_amd.launch_gemm_prefill_w4a16(qw[i % C], sc[i % C], A, None, outp, M, N, K)
+            ms = time_graph(graph_of(fn, C), 3) / C
+            fl = 2.0 * M * N * K
+            tot_flop += fl
+            tot_ms += ms
+            pre.append({"M": M, "shape": f"{name} {K}->{N}", "us": round(ms * 1e3, 2),
+                        "TFLOP/s": round(fl / (ms * 1e-3) / 1e12, 1)})
+            del qw, sc
+        pre.append({"M": M, "shape": "layer total", "TFLOP/s": round(tot_flop / (tot_ms * 1e-3) / 1e12, 1),
+                    "mfma_frac": round(tot_flop / (tot_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)})
+    result["prefill_gemm"] = pre
+
+    # ---------------- CPU baseline: the oracle (port of the CPU golden) ------
+    if not args.no_cpu:
+        import oracle
+        qwc, scc = oracle.synth_w4(7, 2 * I, H)
+        xv = oracle.synth_f16_normal(8, H)
+        q8c, xsc, s8c = oracle.quantize_q8_1(xv)
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            oracle.gemv_swiglu_w4a8(qwc, scc, q8c, xsc, s8c, H, I)
+            reps += 1
+            if time.perf_counter() - t0 > 10.0 or reps >= 2000:
+                break
+        dt = time.perf_counter() - t0
+        result["cpu_baseline"] = {
+            "value": round(b_gu * reps / dt / 1e9, 3),
+            "unit": "GB/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"{reps} x gate+up SwiGLU GEMV 1536->2x8960 (configs[1]'s largest projection) with the "
+                      f"scalar oracle (restated CPU golden, tests/test_kernels.cu:308-363), ~10 s, 1 thread; "
+                      f"host nproc={os.cpu_count()}",
+        }
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,127 @@
+"""GPU parity of the prefill dequant-GEMM family (MFMA) against the oracle.
+
+Reference: src/kernels/gemm_prefill.cu (kernels :319-610, launchers
+:616-684).  fp16 A, fp16 dequantized W, fp32 accumulation, fp16 output;
+residual added as fp16(fp16(acc) + res).  Tolerance: helpers.assert_fp16_close.
+At the full BASELINE configs[3] sizes (M = 512, 1024) the double-precision
+oracle is too slow on the CPU, so the reference there is a plain PyTorch
+fp32 matmul of the oracle-dequantized weights (floating-point kernel).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import assert_fp16_close, dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def qe():
+    import qe_amd
+    qe_amd.lib()
+    return qe_amd
+
+
+def _A(orc, M, K, seed):
+    return orc.synth_f16_normal(seed, M * K).reshape(M, K)
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 1536, 1536), (128, 1536, 8960), (37, 200, 256), (1, 64, 128),
+                                   (300, 130, 384), (16, 2048, 1536), (129, 257, 128)])
+def test_gemm_plain(qe, orc, M, N, K):
+    print(f"gemm M={M} N={N} K={K}", flush=True)
+    qw, sc = orc.synth_w4(M + N + K, N, K)
+    A = _A(orc, M, K, 5)
+    out = empty((M, N), torch.float16)
+    qe.launch_gemm_prefill_w4a16(dev(qw), dev(sc), dev(A), None, out, M, N, K)
+    ref, ex, bd = orc.gemm_w4a16(qw, sc, A, M, N, K)
+    assert_fp16_close(host(out), ex, bd, ref, what=f"gemm {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 1536, 1536), (64, 1536, 8960), (50, 96, 256)])
+def test_gemm_residual_inplace(qe, orc, M, N, K):
+    """O-proj / down-proj of prefill: residual == output (src/engine.cu:500-524)."""
+    qw, sc = orc.synth_w4(7 * N, N, K)
+    A = _A(orc, M, K, 6)
+    R = orc.synth_f16_normal(8, M * N).reshape(M, N)
+    out = dev(R)
+    qe.launch_gemm_prefill_w4a16(dev(qw), dev(sc), dev(A), out, out, M, N, K)
+    got = host(out)
+    ref, ex, bd = orc.gemm_w4a16(qw, sc, A, M, N, K, residual=R)
+    _, acc, _ = orc.gemm_w4a16(qw, sc, A, M, N, K)
+    # fp16(fp16(acc)+res) rounds twice: the first rounding (half an ulp of
+    # acc, or a full ulp when the GPU's fp32 acc lands on the other side of a
+    # rounding boundary) is added to the floor.
+    from helpers import ulp16
+    assert_fp16_close(got, ex, bd + ulp16(acc) * 2.0 ** 20, ref, what="gemm residual")
+
+
+def test_gemm_qkv(qe, orc):
+    M, K, nq, nkv, hd = 128, 1536, 12, 2, 128
+    dims = (nq * hd, nkv * hd, nkv * hd)
+    mats = [orc.synth_w4(300 + i, n, K) for i, n in enumerate(dims)]
+    A = _A(orc, M, K, 9)
+    outs = [empty((M, n), torch.float16) for n in dims]
+    dw = [(dev(w), dev(s)) for w, s in mats]
+    view = qe.make_qkv_view(dw[0][0], dw[0][1], outs[0], dw[1][0], dw[1][1], outs[1], dw[2][0], dw[2][1], outs[2])
+    qe.launch_gemm_prefill_qkv_w4a16(view, dev(A), M, in_features=K, num_q_heads=nq, num_kv_heads=nkv, head_dim=hd)
+    for (w, s), o, n in zip(mats, outs, dims):
+        ref, ex, bd = orc.gemm_w4a16(w, s, A, M, n, K)
+        assert_fp16_close(host(o), ex, bd, ref, what="gemm qkv")
+
+
+def test_gemm_qkv_ragged_heads(qe, orc):
+    """Head counts whose column ranges do not align with the tiles."""
+    M, K, nq, nkv, hd = 70, 256, 3, 1, 40
+    dims = (nq * hd, nkv * hd, nkv * hd)
+    mats = [orc.synth_w4(400 + i, n, K) for i, n in enumerate(dims)]
+    A = _A(orc, M, K, 10)
+    outs = [empty((M, n), torch.float16) for n in dims]
+    dw = [(dev(w), dev(s)) for w, s in mats]
+    view = qe.make_qkv_view(dw[0][0], dw[0][1], outs[0], dw[1][0], dw[1][1], outs[1], dw[2][0], dw[2][1], outs[2])
+    qe.launch_gemm_prefill_qkv_w4a16(view, dev(A), M, in_features=K, num_q_heads=nq, num_kv_heads=nkv, head_dim=hd)
+    for (w, s), o, n in zip(mats, outs, dims):
+        ref, ex, bd = orc.gemm_w4a16(w, s, A, M, n, K)
+        assert_fp16_close(host(o), ex, bd, ref, what="gemm qkv ragged")
+
+
+@pytest.mark.parametrize("M,I,K", [(128, 8960, 1536), (33, 100, 256)])
+def test_gemm_swiglu(qe, orc, M, I, K):
+    print(f"gemm swiglu M={M} I={I}", flush=True)
+    qw, sc = orc.synth_w4(500 + I, 2 * I, K)
+    A = _A(orc, M, K, 11)
+    out = empty((M, I), torch.float16)
+    qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a16(dev(qw), dev(sc), dev(A), out, M, hidden_size=K,
+                                                     intermediate_size=I)
+    ref, ex, bd = orc.gemm_swiglu_w4a16(qw, sc, A, M, K, I)
+    assert_fp16_close(host(out), ex, bd, ref, what="gemm swiglu")
+
+
+def _torch_ref(orc, qw, sc, A, N, K):
+    wdq = torch.from_numpy(orc.dequant_w4_f16(qw, sc, N, K)).cuda().float()
+    a = torch.from_numpy(A).cuda().float()
+    acc = (a @ wdq.T).double()
+    bound = (a.abs() @ wdq.abs().T).double()
+    return acc.cpu().numpy(), bound.cpu().numpy()
+
+
+@pytest.mark.parametrize("M", [512, 1024])
+@pytest.mark.parametrize("N,K", [(2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960)])
+def test_gemm_full_configs(qe, orc, M, N, K):
+    """configs[3] at full size: fp32 torch matmul of the dequantized weights."""
+    print(f"gemm full M={M} N={N} K={K}", flush=True)
+    qw, sc = orc.synth_w4(N + K, N, K)
+    A = _A(orc, M, K, M)
+    out = empty((M, N), torch.float16)
+    qe.launch_gemm_prefill_w4a16(dev(qw), dev(sc), dev(A), None, out, M, N, K)
+    ex, bd = _torch_ref(orc, qw, sc, A, N, K)
+    # the fp32 torch reference itself carries ~K*2^-24*bound error: widen the floor
+    assert_fp16_close(host(out), ex, bd * 4, ex.astype(np.float32).astype(np.float16), min_identical=0.9,
+                      what="gemm full")
+
+
+def test_gemm_rejects_bad_k(qe):
+    with pytest.raises(RuntimeError, match="multiple of 128"):
+        qe.launch_gemm_prefill_w4a16(empty(10, torch.int32), empty(10, torch.float16), empty(100, torch.float16),
+                                     None, empty(4, torch.float16), 1, 4, 100)
