@@ -109,6 +109,24 @@ int qe_launch_gemv_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_qweight, co
                                              const uint16_t* input_x, uint16_t* output_mlp,
                                              int hidden_size, int intermediate_size, hipStream_t stream);
 
+/* ---- fused decode entry points (no counterpart in the reference API) ---- */
+
+/* RMSNorm + Q8_1 + fused-QKV GEMV in one launch: the same results as
+ * qe_launch_rmsnorm_q8_1 followed by qe_launch_gemv_qkv_w4a8 (the reference's
+ * src/engine.cu:367-379 pair), without the Q8_1 round trip through memory.
+ * output_fp16_opt (optional) receives the fp16 normalized activation. */
+int qe_launch_rmsnorm_gemv_qkv_w4a16(const uint16_t* input, const uint16_t* gamma, uint16_t* output_fp16_opt,
+                                     const qe_qkv_view* view, hipStream_t stream, int hidden_size,
+                                     int num_q_heads, int num_kv_heads, int head_dim);
+
+/* RMSNorm + Q8_1 + gate/up SwiGLU GEMV in one launch: the same results as
+ * qe_launch_rmsnorm_q8_1 followed by qe_launch_gemv_dual_gate_up_swiglu_w4a8
+ * (src/engine.cu:414-424). */
+int qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(const uint16_t* input, const uint16_t* gamma,
+                                                     uint16_t* output_fp16_opt, const uint32_t* gate_up_qweight,
+                                                     const uint16_t* gate_up_scales, uint16_t* output_mlp,
+                                                     int hidden_size, int intermediate_size, hipStream_t stream);
+
 /* ---- prefill dequant-GEMM (MFMA) ----------------------------------------- */
 
 /* Replaces launch_gemm_prefill_w4a16, include/kernels.cuh:119-130.

@@ -1,23 +1,31 @@
 // W4A8 / W4A16 group-128 decode GEMV family for gfx950.
 //
 // Math (bit-for-bit on the integer stage) of src/kernels/gemv_w4a16.cu:
-//   per 32-element chunk: dot = sum of 4 dp4a_w4_q8_oct (sum8-seeded),
+//   per 32-element chunk: dot = sum of 4 dp4a_w4_q8_oct seeded with sum8,
 //   acc += float(dot) * (float(w_scale) * x_scale),  y = fp16(acc [+ res]).
+// The four sum8 seeds of a chunk are added before the dot (integer
+// addition, so the dot is unchanged).
 //
-// Layout of the work (MI355X-first, not the reference's 8-lane sub-warps):
-//   * A "segment" of LPR lanes (LPR in 8..64, a power of two inside one
-//     wave64) owns one output row (two for SwiGLU).  Lane l of the segment
-//     owns the 32-element chunks c = l + i*LPR, i < NCH, of every row.
-//   * Each lane keeps the Q8_1 activation of its chunks in VGPRs for the
-//     whole kernel (13 dwords per chunk), so the weight stream is the only
-//     per-row memory traffic: one 16-byte global_load_dwordx4 per chunk,
-//     fully coalesced (16*LPR contiguous bytes per segment per load).
-//   * Partial sums are reduced inside the segment with DPP row operations
-//     (quad_perm, row_half_mirror, row_mirror) and ds_swizzle for 32 lanes.
-//   * Blocks are 256 threads; the grid is capped at 8 blocks per CU and
-//     loops over row sets, so x is staged once per block.
-// Shapes the fast kernel does not cover (unaligned weights, K > 16384)
-// go to a generic wave-per-row kernel with x staged in LDS.
+// Work layout (MI355X-first; these launches are latency-bound, so the
+// critical path is kept to one round of loads):
+//   * A "segment" of LPR lanes (16 or 64, inside one wave64) owns RPS
+//     consecutive weight rows per iteration; lane l owns the 32-element
+//     chunks c = l + i*LPR (i < NCH) of every row, so the only per-row
+//     traffic is one 16-byte global_load_dwordx4 (nt) per chunk plus the
+//     fp16 scale.  Segment loads are contiguous (16*LPR bytes).
+//   * Q8_1 activations (W4A8): each lane loads just its own chunks straight
+//     into VGPRs - no LDS, no barrier.  fp16 activations (W4A16, and the
+//     fused RMSNorm entry points): the 256-thread block quantizes the vector
+//     once, 8 elements per thread (a 128-group is one 16-lane DPP row), into
+//     LDS, and each lane then reads its chunks.
+//   * The first row set's weights are requested at kernel entry, before
+//     the activation, and each iteration prefetches the next row set.
+//   * Partial sums are reduced in the segment with DPP row operations
+//     (quad_perm, row_half_mirror, row_mirror), ds_swizzle for 32 lanes.
+//   * 64-thread blocks unless the matrix is large enough for 256-thread
+//     persistent blocks (grid capped per CU).
+// Shapes outside the fast kernel (weights not 16-byte aligned, K > 16384)
+// use a generic wave-per-row kernel that stages Q8_1 in LDS.
 #include "qe_common.hpp"
 
 namespace qe {
@@ -27,321 +35,519 @@ constexpr int kPlain = 0;
 constexpr int kQKV = 1;
 constexpr int kSwiglu = 2;
 
+constexpr int kXQ8 = 0;   // Q8_1 activation
+constexpr int kXF16 = 1;  // fp16 activation, quantized in the block
+constexpr int kXRMS = 2;  // fp16 activation, RMSNorm then quantized in the block
+
+constexpr float kRmsEps = 1e-6f;  // RMS_NORM_EPS, include/config.cuh:20
+
 struct GemvParams {
     const uint32_t* qw[3];
     const uint16_t* sc[3];
     uint16_t* out[3];
-    int row_begin[3];  // first virtual row of each matrix (QKV mode)
+    int row_begin[3];  // first physical row of each matrix (QKV mode)
     const uint16_t* residual;
     const int8_t* q8;
     const float* xs;
     const int32_t* s8;
-    const uint16_t* x16;  // fp16 activation (W4A16 entry points)
-    int n_out;            // output rows (SwiGLU: intermediate features)
+    const uint16_t* x16;    // fp16 activation (kXF16 / kXRMS)
+    const uint16_t* gamma;  // RMSNorm weight (kXRMS)
+    uint16_t* norm_out;     // optional fp16 normalized activation (kXRMS, block 0 writes)
+    int n_rows;             // physical weight rows
     int K;
 };
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-// fp16 x -> Q8_1 in LDS, 16 lanes per group, whole block (256 threads).
-__device__ __forceinline__ void quantize_x_to_lds(const uint16_t* __restrict__ x, int K, int8_t* s_q8,
-                                                  int32_t* s_s8, float* s_xs) {
-    const int G = K >> 7;
-    const int sub = threadIdx.x & 15;
-    for (int g = threadIdx.x >> 4; g < G; g += (blockDim.x >> 4)) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(x + g * 128 + sub * 8);
-        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-        float vals[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            vals[2 * j] = h2f(static_cast<uint16_t>(w[j] & 0xFFFFu));
-            vals[2 * j + 1] = h2f(static_cast<uint16_t>(w[j] >> 16));
-        }
-        const qwen::Q8Group q = qwen::quantize_group128_q8_1(vals);
-        *reinterpret_cast<int2*>(s_q8 + g * 128 + sub * 8) = make_int2(q.x_lo, q.x_hi);
-        s_s8[g * 16 + sub] = q.sum8;
-        if (sub == 0) s_xs[g] = q.d;
-    }
-}
-
-__device__ __forceinline__ int32_t chunk_dot(const u32x4 w, const int4 xa, const int4 xb, const int4 s8) {
-    return qwen::dp4a_w4_q8_oct(w.x, xa.x, xa.y, s8.x) + qwen::dp4a_w4_q8_oct(w.y, xa.z, xa.w, s8.y) +
-           qwen::dp4a_w4_q8_oct(w.z, xb.x, xb.y, s8.z) + qwen::dp4a_w4_q8_oct(w.w, xb.z, xb.w, s8.w);
-}
-
-template <int LPR, int NCH, int MODE, bool F16IN>
-__global__ __launch_bounds__(256) void gemv_w4_kernel(GemvParams p) {
-    constexpr int SEGS = 256 / LPR;
-    const int K = p.K;
-    const int KC = K >> 5;
-    const int G = K >> 7;
-    const int seg = threadIdx.x / LPR;
-    const int l = threadIdx.x % LPR;
-
-    // ---- activation slice of this lane, kept in VGPRs --------------------
-    const int8_t* q8 = p.q8;
-    const int32_t* s8 = p.s8;
-    const float* xs = p.xs;
-    if constexpr (F16IN) {
-        extern __shared__ __align__(16) uint8_t s_mem[];
-        int8_t* s_q8 = reinterpret_cast<int8_t*>(s_mem);
-        int32_t* s_s8 = reinterpret_cast<int32_t*>(s_mem + K);
-        float* s_xs = reinterpret_cast<float*>(s_mem + K + (K >> 3) * 4);
-        quantize_x_to_lds(p.x16, K, s_q8, s_s8, s_xs);
+template <int BT>
+__device__ __forceinline__ float block_sum(float v, float* s_red) {
+    v = qwen::seg_sum<64>(v);
+    if constexpr (BT == 64) {
+        return v;
+    } else {
+        if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
         __syncthreads();
-        q8 = s_q8;
-        s8 = s_s8;
-        xs = s_xs;
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < BT / 64; ++w) t += s_red[w];
+        return t;
     }
-    int4 xa[NCH], xb[NCH], xsum[NCH];
-    float xd[NCH];
+}
+
+__device__ __forceinline__ void unpack8(const uint4 raw, float vals[8]) {
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        vals[2 * j] = h2f(static_cast<uint16_t>(w[j] & 0xFFFFu));
+        vals[2 * j + 1] = h2f(static_cast<uint16_t>(w[j] >> 16));
+    }
+}
+
+__device__ __forceinline__ uint4 load8_f16(const uint16_t* p, bool vec) {
+    if (vec) return *reinterpret_cast<const uint4*>(p);
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = static_cast<uint32_t>(p[2 * j]) | (static_cast<uint32_t>(p[2 * j + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// fp16(fp16(x*h)*g) for 8 packed values: the two fp16 multiplies of the
+// reference RMSNorm (src/kernels/rmsnorm_rope.cu:214-227).
+__device__ __forceinline__ uint4 rms_apply8(uint4 xv, uint4 gv, _Float16 h) {
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const qwen::qe_half2_t hh = {h, h};
+        qwen::qe_half2_t n = __builtin_bit_cast(qwen::qe_half2_t, xw[j]) * hh;
+        n = n * __builtin_bit_cast(qwen::qe_half2_t, gw[j]);
+        o[j] = __builtin_bit_cast(uint32_t, n);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// Stage the activation of the whole block in LDS: s_q8[K] and, per
+// 32-element chunk, s_rec[c] = {sum8[4c..4c+3] summed, bits of x_scale}.
+// VEC: 16-byte vector loads are legal for the activation buffers.
+template <int XM, int BT, bool VEC>
+__device__ __forceinline__ void stage_activation(const GemvParams& p, int8_t* s_q8, int2* s_rec, float* s_red) {
+    const int K = p.K;
+    const int G = K >> 7;
+    if constexpr (XM == kXQ8) {
+        if (VEC) {
+            for (int i = threadIdx.x; i < (K >> 4); i += BT)
+                reinterpret_cast<uint4*>(s_q8)[i] = reinterpret_cast<const uint4*>(p.q8)[i];
+        } else {
+            for (int i = threadIdx.x; i < K; i += BT) s_q8[i] = p.q8[i];
+        }
+        for (int c = threadIdx.x; c < (K >> 5); c += BT) {
+            const int32_t* s = p.s8 + 4 * c;
+            s_rec[c] = make_int2(s[0] + s[1] + s[2] + s[3], __builtin_bit_cast(int, p.xs[c >> 2]));
+        }
+    } else {
+        _Float16 h = static_cast<_Float16>(0.0f);
+        if constexpr (XM == kXRMS) {
+            float ss = 0.0f;
+            for (int i = threadIdx.x; i < (K >> 3); i += BT) {
+                float v[8];
+                unpack8(load8_f16(p.x16 + 8 * i, VEC), v);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
+            }
+            const float total = block_sum<BT>(ss, s_red);
+            h = static_cast<_Float16>(1.0f / sqrtf(total / static_cast<float>(K) + kRmsEps));
+        }
+        const int sub = threadIdx.x & 15;
+        for (int g = threadIdx.x >> 4; g < G; g += BT / 16) {
+            uint4 raw = load8_f16(p.x16 + g * 128 + sub * 8, VEC);
+            if constexpr (XM == kXRMS) {
+                raw = rms_apply8(raw, load8_f16(p.gamma + g * 128 + sub * 8, VEC), h);
+                if (p.norm_out != nullptr && blockIdx.x == 0) {
+                    uint16_t* o = p.norm_out + g * 128 + sub * 8;
+                    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        o[2 * j] = static_cast<uint16_t>(w[j] & 0xFFFFu);
+                        o[2 * j + 1] = static_cast<uint16_t>(w[j] >> 16);
+                    }
+                }
+            }
+            float vals[8];
+            unpack8(raw, vals);
+            const qwen::Q8Group q = qwen::quantize_group128_q8_1(vals);
+            *reinterpret_cast<int2*>(s_q8 + g * 128 + sub * 8) = make_int2(q.x_lo, q.x_hi);
+            // chunk j of the group = lanes 4j..4j+3 of the 16-lane row
+            int csum = q.sum8;
+            csum += qwen::dpp_i32<0xB1>(csum);
+            csum += qwen::dpp_i32<0x4E>(csum);
+            if ((sub & 3) == 0) s_rec[g * 4 + (sub >> 2)] = make_int2(csum, __builtin_bit_cast(int, q.d));
+        }
+    }
+}
+
+__device__ __forceinline__ int32_t chunk_dot(const u32x4 w, const int4 xa, const int4 xb, int32_t seed) {
+    int32_t d = qwen::dp4a_w4_q8_oct(w.x, xa.x, xa.y, seed);
+    d = qwen::dp4a_w4_q8_oct(w.y, xa.z, xa.w, d);
+    d = qwen::dp4a_w4_q8_oct(w.z, xb.x, xb.y, d);
+    return qwen::dp4a_w4_q8_oct(w.w, xb.z, xb.w, d);
+}
+
+template <int MODE>
+__device__ __forceinline__ void row_ptrs(const GemvParams& p, int row, const u32x4*& w, const uint16_t*& s, int& m,
+                                         int& local) {
+    m = 0;
+    local = row;
+    if constexpr (MODE == kQKV) {
+        m = (row >= p.row_begin[1]) + (row >= p.row_begin[2]);
+        local = row - p.row_begin[m];
+    }
+    w = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(local) * (p.K >> 3));
+    s = p.sc[m] + static_cast<size_t>(local) * (p.K >> 7);
+}
+
+// Q8_1 activation slice of lane l of a segment, straight from global:
+// chunks c = l + i*LPR, i < NCH, as q8 (xa, xb), the chunk's summed sum8
+// seed and the group scale.  Chunks past K get a zero slice.  All loads are
+// issued before any use.
+template <int LPR, int NCH>
+__device__ __forceinline__ void load_x_slice_q8(const GemvParams& p, int l, int4 (&xa)[NCH], int4 (&xb)[NCH],
+                                                int32_t (&xsum)[NCH], float (&xd)[NCH]) {
+    const int KC = p.K >> 5;
+    int4 s4[NCH];
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-        const int c = l + i * LPR;
-        if (c < KC) {
-            xa[i] = *reinterpret_cast<const int4*>(q8 + c * 32);
-            xb[i] = *reinterpret_cast<const int4*>(q8 + c * 32 + 16);
-            xsum[i] = *reinterpret_cast<const int4*>(s8 + c * 4);
-            xd[i] = xs[c >> 2];
-        } else {
-            xa[i] = xb[i] = xsum[i] = make_int4(0, 0, 0, 0);
+        const int cc = min(l + i * LPR, KC - 1);
+        xa[i] = *reinterpret_cast<const int4*>(p.q8 + cc * 32);
+        xb[i] = *reinterpret_cast<const int4*>(p.q8 + cc * 32 + 16);
+        s4[i] = *reinterpret_cast<const int4*>(p.s8 + cc * 4);
+        xd[i] = p.xs[cc >> 2];
+    }
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        xsum[i] = s4[i].x + s4[i].y + s4[i].z + s4[i].w;
+        if (l + i * LPR >= KC) {
+            xa[i] = xb[i] = make_int4(0, 0, 0, 0);
+            xsum[i] = 0;
             xd[i] = 0.0f;
         }
     }
+}
 
-    const int stride = SEGS * gridDim.x;
-    for (int r = blockIdx.x * SEGS + seg; r < p.n_out; r += stride) {
-        if constexpr (MODE == kSwiglu) {
-            const size_t rg = static_cast<size_t>(2 * r);
-            const u32x4* wg = reinterpret_cast<const u32x4*>(p.qw[0] + rg * (K >> 3));
-            const u32x4* wu = reinterpret_cast<const u32x4*>(p.qw[0] + (rg + 1) * (K >> 3));
-            const uint16_t* sg = p.sc[0] + rg * G;
-            const uint16_t* su = p.sc[0] + (rg + 1) * G;
-            u32x4 w0[NCH], w1[NCH];
-            uint16_t h0[NCH], h1[NCH];
+// fp16 activation staged by the whole block: thread t quantizes the 8
+// elements 8u..8u+7 for u = t + BT*j (a 128-group is one 16-lane DPP row,
+// the quantizer is quantize_group128_q8_1), RMS-normalizing first for kXRMS.
+// All global loads are issued before any arithmetic.  Output in LDS: q8[K]
+// and per 32-element chunk {summed sum8 of its 4 words, scale}.
+template <int XM, int BT, int MAXP>
+__device__ __forceinline__ void stage_block_f16(const GemvParams& p, int8_t* s_q8, int2* s_rec, float* s_red) {
+    const int K = p.K;
+    const int U = K >> 3;  // 8-element units
+    const int t = threadIdx.x;
+    uint4 raw[MAXP];
 #pragma unroll
-            for (int i = 0; i < NCH; ++i) {
-                const int c = min(l + i * LPR, KC - 1);  // clamped: no branches around the loads
-                w0[i] = __builtin_nontemporal_load(wg + c);
-                w1[i] = __builtin_nontemporal_load(wu + c);
-                h0[i] = sg[c >> 2];
-                h1[i] = su[c >> 2];
-            }
-            float ag = 0.0f, au = 0.0f;
+    for (int j = 0; j < MAXP; ++j) {
+        const int u = min(t + BT * j, U - 1);
+        raw[j] = *reinterpret_cast<const uint4*>(p.x16 + 8 * u);
+    }
+    if constexpr (XM == kXRMS) {
+        uint4 graw[MAXP];
 #pragma unroll
-            for (int i = 0; i < NCH; ++i) {  // out-of-range chunks have a zero x slice
-                ag += static_cast<float>(chunk_dot(w0[i], xa[i], xb[i], xsum[i])) * (h2f(h0[i]) * xd[i]);
-                au += static_cast<float>(chunk_dot(w1[i], xa[i], xb[i], xsum[i])) * (h2f(h1[i]) * xd[i]);
-            }
-            ag = qwen::seg_sum<LPR>(ag);
-            au = qwen::seg_sum<LPR>(au);
-            if (l == 0) p.out[0][r] = f2h(silu_mul(ag, au));
-        } else {
-            int m = 0;
-            int row = r;
-            if constexpr (MODE == kQKV) {
-                m = (r >= p.row_begin[1]) + (r >= p.row_begin[2]);
-                row = r - p.row_begin[m];
-            }
-            const u32x4* wr = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(row) * (K >> 3));
-            const uint16_t* sr = p.sc[m] + static_cast<size_t>(row) * G;
-            u32x4 w0[NCH];
-            uint16_t h0[NCH];
+        for (int j = 0; j < MAXP; ++j) {
+            const int u = min(t + BT * j, U - 1);
+            graw[j] = *reinterpret_cast<const uint4*>(p.gamma + 8 * u);
+        }
+        float ss = 0.0f;
 #pragma unroll
-            for (int i = 0; i < NCH; ++i) {
-                const int c = min(l + i * LPR, KC - 1);
-                w0[i] = __builtin_nontemporal_load(wr + c);
-                h0[i] = sr[c >> 2];
-            }
-            float acc = 0.0f;
+        for (int j = 0; j < MAXP; ++j) {
+            if (t + BT * j < U) {
+                float v[8];
+                unpack8(raw[j], v);
 #pragma unroll
-            for (int i = 0; i < NCH; ++i)
-                acc += static_cast<float>(chunk_dot(w0[i], xa[i], xb[i], xsum[i])) * (h2f(h0[i]) * xd[i]);
-            acc = qwen::seg_sum<LPR>(acc);
-            if (l == 0) {
-                if (MODE == kPlain && p.residual != nullptr) acc += h2f(p.residual[row]);
-                p.out[m][row] = f2h(acc);
+                for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+            }
+        }
+        const float total = block_sum<BT>(ss, s_red);
+        const _Float16 h = static_cast<_Float16>(1.0f / sqrtf(total / static_cast<float>(K) + kRmsEps));
+        const bool write_norm = p.norm_out != nullptr && blockIdx.x == 0;
+#pragma unroll
+        for (int j = 0; j < MAXP; ++j) {
+            raw[j] = rms_apply8(raw[j], graw[j], h);
+            if (write_norm && t + BT * j < U) *reinterpret_cast<uint4*>(p.norm_out + 8 * (t + BT * j)) = raw[j];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < MAXP; ++j) {
+        if (BT * j < U) {  // 16-lane rows are whole groups: they enter or skip together
+            const int u = t + BT * j;
+            if (u < U) {
+                float vals[8];
+                unpack8(raw[j], vals);
+                const qwen::Q8Group q = qwen::quantize_group128_q8_1(vals);
+                *reinterpret_cast<int2*>(s_q8 + 8 * u) = make_int2(q.x_lo, q.x_hi);
+                int csum = q.sum8;  // chunk = the 4 words of a DPP quad
+                csum += qwen::dpp_i32<0xB1>(csum);
+                csum += qwen::dpp_i32<0x4E>(csum);
+                if ((u & 3) == 0) s_rec[u >> 2] = make_int2(csum, __builtin_bit_cast(int, q.d));
             }
         }
     }
 }
 
-// Generic kernel: one wave per output row (pair), dword weight loads, Q8_1
-// staged in LDS with scalar copies.  Covers any K % 128 == 0 up to the LDS
-// limit and any 4-byte weight alignment (the reference's uint32 fallback,
+template <int BT, int LPR, int NCH, int RPS, int MODE, int XM>
+__global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
+    static_assert(MODE != kSwiglu || RPS == 2, "SwiGLU segments own a (gate, up) row pair");
+    constexpr int SEGS = BT / LPR;
+    const int K = p.K;
+    const int KC = K >> 5;
+    const int seg = threadIdx.x / LPR;
+    const int l = threadIdx.x % LPR;
+    const int n_sets = (p.n_rows + RPS - 1) / RPS;
+    const int set_stride = SEGS * gridDim.x;
+
+    // ---- request the first row set before anything else --------------------
+    int set = blockIdx.x * SEGS + seg;
+    u32x4 w[RPS][NCH];
+    uint16_t hs[RPS][NCH];
+    auto load_set = [&](int st, u32x4 (&wr)[RPS][NCH], uint16_t (&hr)[RPS][NCH]) {
+#pragma unroll
+        for (int r = 0; r < RPS; ++r) {
+            const int row = min(st * RPS + r, p.n_rows - 1);  // clamped: tail rows are loaded, not stored
+            const u32x4* wp;
+            const uint16_t* sp;
+            int m, local;
+            row_ptrs<MODE>(p, row, wp, sp, m, local);
+#pragma unroll
+            for (int i = 0; i < NCH; ++i) {
+                const int c = min(l + i * LPR, KC - 1);
+                wr[r][i] = __builtin_nontemporal_load(wp + c);
+                hr[r][i] = sp[c >> 2];
+            }
+        }
+    };
+    if (set < n_sets) load_set(set, w, hs);
+
+    // ---- activation slice in VGPRs ---------------------------------------------
+    int4 xa[NCH], xb[NCH];
+    int32_t xsum[NCH];
+    float xd[NCH];
+    if constexpr (XM == kXQ8) {
+        load_x_slice_q8<LPR, NCH>(p, l, xa, xb, xsum, xd);
+    } else {
+        extern __shared__ __align__(16) uint8_t s_mem[];
+        __shared__ float s_red[BT / 64];
+        int8_t* s_q8 = reinterpret_cast<int8_t*>(s_mem);
+        int2* s_rec = reinterpret_cast<int2*>(s_mem + K);
+        // K <= 32 * LPR * NCH, i.e. at most LPR*NCH*4 8-element units
+        stage_block_f16<XM, BT, (LPR * NCH * 4 + BT - 1) / BT>(p, s_q8, s_rec, s_red);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int c = l + i * LPR;
+            const int cc = min(c, KC - 1);
+            xa[i] = *reinterpret_cast<const int4*>(s_q8 + cc * 32);
+            xb[i] = *reinterpret_cast<const int4*>(s_q8 + cc * 32 + 16);
+            const int2 rec = s_rec[cc];
+            xsum[i] = rec.x;
+            xd[i] = __builtin_bit_cast(float, rec.y);
+            if (c >= KC) {
+                xa[i] = xb[i] = make_int4(0, 0, 0, 0);
+                xsum[i] = 0;
+                xd[i] = 0.0f;
+            }
+        }
+    }
+
+    // ---- stream row sets -----------------------------------------------------
+    for (; set < n_sets; set += set_stride) {
+        u32x4 wn[RPS][NCH];
+        uint16_t hn[RPS][NCH];
+        const int next = set + set_stride;
+        if (next < n_sets) load_set(next, wn, hn);
+        float acc[RPS];
+#pragma unroll
+        for (int r = 0; r < RPS; ++r) {
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NCH; ++i)
+                a += static_cast<float>(chunk_dot(w[r][i], xa[i], xb[i], xsum[i])) * (h2f(hs[r][i]) * xd[i]);
+            acc[r] = qwen::seg_sum<LPR>(a);
+        }
+        if (l == 0) {
+            if constexpr (MODE == kSwiglu) {
+                p.out[0][set] = f2h(silu_mul(acc[0], acc[1]));
+            } else {
+#pragma unroll
+                for (int r = 0; r < RPS; ++r) {
+                    const int row = set * RPS + r;
+                    if (row < p.n_rows) {
+                        const u32x4* wp;
+                        const uint16_t* sp;
+                        int m, local;
+                        row_ptrs<MODE>(p, row, wp, sp, m, local);
+                        float v = acc[r];
+                        if (MODE == kPlain && p.residual != nullptr) v += h2f(p.residual[local]);
+                        p.out[m][local] = f2h(v);
+                    }
+                }
+            }
+        }
+        if (next < n_sets) {
+#pragma unroll
+            for (int r = 0; r < RPS; ++r)
+#pragma unroll
+                for (int i = 0; i < NCH; ++i) {
+                    w[r][i] = wn[r][i];
+                    hs[r][i] = hn[r][i];
+                }
+        }
+    }
+}
+
+// Generic kernel: one wave per output (row or SwiGLU pair), dword weight
+// loads, scalar staging.  Covers any K % 128 == 0 up to the LDS limit and any
+// 4-byte weight alignment (the reference's uint32 fallback,
 // src/kernels/gemv_w4a16.cu:264-630).
-template <int MODE, bool F16IN>
+template <int MODE, int XM>
 __global__ __launch_bounds__(256) void gemv_w4_generic_kernel(GemvParams p) {
     extern __shared__ __align__(16) uint8_t s_mem[];
+    __shared__ float s_red[4];
     const int K = p.K;
-    const int G = K >> 7;
     const int KW = K >> 3;
     int8_t* s_q8 = reinterpret_cast<int8_t*>(s_mem);
-    int32_t* s_s8 = reinterpret_cast<int32_t*>(s_mem + K);
-    float* s_xs = reinterpret_cast<float*>(s_mem + K + KW * 4);
-    if constexpr (F16IN) {
-        const int sub = threadIdx.x & 15;
-        for (int g = threadIdx.x >> 4; g < G; g += 16) {
-            float vals[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) vals[j] = h2f(p.x16[g * 128 + sub * 8 + j]);
-            const qwen::Q8Group q = qwen::quantize_group128_q8_1(vals);
-            reinterpret_cast<int32_t*>(s_q8)[(g * 128 + sub * 8) / 4] = q.x_lo;
-            reinterpret_cast<int32_t*>(s_q8)[(g * 128 + sub * 8) / 4 + 1] = q.x_hi;
-            s_s8[g * 16 + sub] = q.sum8;
-            if (sub == 0) s_xs[g] = q.d;
-        }
-    } else {
-        for (int i = threadIdx.x; i < K; i += blockDim.x) s_q8[i] = p.q8[i];
-        for (int i = threadIdx.x; i < KW; i += blockDim.x) s_s8[i] = p.s8[i];
-        for (int i = threadIdx.x; i < G; i += blockDim.x) s_xs[i] = p.xs[i];
-    }
+    int2* s_rec = reinterpret_cast<int2*>(s_mem + K);
+    stage_activation<XM, 256, false>(p, s_q8, s_rec, s_red);
     __syncthreads();
     const int wave = threadIdx.x >> 6;
     const int l = threadIdx.x & 63;
-    const int stride = 4 * gridDim.x;
     const int32_t* xq = reinterpret_cast<const int32_t*>(s_q8);
-    for (int r = blockIdx.x * 4 + wave; r < p.n_out; r += stride) {
-        const int nrows = (MODE == kSwiglu) ? 2 : 1;
-        float acc[2] = {0.0f, 0.0f};
-        int m = 0;
-        int row = r;
-        if constexpr (MODE == kQKV) {
-            m = (r >= p.row_begin[1]) + (r >= p.row_begin[2]);
-            row = r - p.row_begin[m];
-        }
-        for (int k = 0; k < nrows; ++k) {
-            const size_t rr = (MODE == kSwiglu) ? static_cast<size_t>(2 * r + k) : static_cast<size_t>(row);
-            const uint32_t* wr = p.qw[m] + rr * KW;
-            const uint16_t* sr = p.sc[m] + rr * G;
+    const int n_out = (MODE == kSwiglu) ? p.n_rows / 2 : p.n_rows;
+    for (int o = blockIdx.x * 4 + wave; o < n_out; o += 4 * gridDim.x) {
+        constexpr int NR = (MODE == kSwiglu) ? 2 : 1;
+        float acc[NR];
+        int m = 0, local = o;
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            const int row = (MODE == kSwiglu) ? 2 * o + k : o;
+            const u32x4* wv;
+            const uint16_t* sp;
+            row_ptrs<MODE>(p, row, wv, sp, m, local);
+            const uint32_t* wr = reinterpret_cast<const uint32_t*>(wv);
             float a = 0.0f;
-            for (int w = l; w < KW; w += 64) {
-                const int32_t d = qwen::dp4a_w4_q8_oct(wr[w], xq[2 * w], xq[2 * w + 1], s_s8[w]);
-                a += static_cast<float>(d) * (h2f(sr[w >> 4]) * s_xs[w >> 4]);
+            // word wd covers elements 8wd..8wd+7: chunk wd/4, group wd/16.  The
+            // chunk's pre-summed sum8 seeds the first word of the chunk only.
+            for (int wd = l; wd < KW; wd += 64) {
+                const int2 rec = s_rec[wd >> 2];
+                const int32_t seed = (wd & 3) == 0 ? rec.x : 0;
+                const int32_t d = qwen::dp4a_w4_q8_oct(wr[wd], xq[2 * wd], xq[2 * wd + 1], seed);
+                a += static_cast<float>(d) * (h2f(sp[wd >> 4]) * __builtin_bit_cast(float, rec.y));
             }
             acc[k] = qwen::seg_sum<64>(a);
         }
         if (l == 0) {
             if constexpr (MODE == kSwiglu) {
-                p.out[0][r] = f2h(silu_mul(acc[0], acc[1]));
+                p.out[0][o] = f2h(silu_mul(acc[0], acc[NR - 1]));
             } else {
                 float v = acc[0];
-                if (MODE == kPlain && p.residual != nullptr) v += h2f(p.residual[row]);
-                p.out[m][row] = f2h(v);
+                if (MODE == kPlain && p.residual != nullptr) v += h2f(p.residual[local]);
+                p.out[m][local] = f2h(v);
             }
         }
     }
 }
 
 constexpr int kMaxFastK = 64 * 8 * 32;   // LPR 64 x 8 chunks x 32 elements
-constexpr int kMaxGenericK = 32768;      // Q8_1 staging: 1.53 B per element of LDS
+constexpr int kMaxGenericK = 32768;      // LDS: K + K/4 bytes
 
-// LPR: the widest segment that still gives each lane >= 3 chunks (enough
-// independent 16-byte loads in flight per lane); NCH rounded up to an
-// instantiated register budget.
 struct Plan {
-    int lpr;
-    int nch;
+    int bt, lpr, nch, rps;
 };
 
-Plan plan_for(int K) {
+Plan plan_for(int K, int n_rows, int mode, bool f16_input) {
     const int KC = K / 32;
-    int lpr = 8;
-    for (int c : {64, 32, 16, 8}) {
-        if ((KC + c - 1) / c >= 3) { lpr = c; break; }
-    }
-    int nch = (KC + lpr - 1) / lpr;
-    static const int kNch[] = {1, 2, 3, 4, 5, 6, 8};
-    for (int n : kNch) {
-        if (n >= nch) { nch = n; break; }
-    }
-    return {lpr, nch};
-}
-
-template <int MODE, bool F16IN, int LPR>
-hipError_t launch_lpr(int nch, const GemvParams& p, int grid, size_t lds, hipStream_t s) {
-    switch (nch) {
-#define QE_NCH(N) \
-    case N: gemv_w4_kernel<LPR, N, MODE, F16IN><<<grid, 256, lds, s>>>(p); break;
-        QE_NCH(1) QE_NCH(2) QE_NCH(3) QE_NCH(4) QE_NCH(5) QE_NCH(6) QE_NCH(8)
-#undef QE_NCH
-        default: return hipErrorInvalidValue;
-    }
-    return hipSuccess;
-}
-
-template <int MODE, bool F16IN>
-int launch_gemv(const GemvParams& p, bool fast_ok, hipStream_t stream, const char* what) {
-    const int K = p.K;
-    if (p.n_out <= 0) return QE_OK;
-    const int max_grid = cu_count() * 8;
-    if (fast_ok && K <= kMaxFastK) {
-        const Plan pl = plan_for(K);
-        const int segs = 256 / pl.lpr;
-        int grid = (p.n_out + segs - 1) / segs;
-        if (grid > max_grid) grid = max_grid;
-        const size_t lds = F16IN ? static_cast<size_t>(K) + K / 2 + K / 32 : 0;
-        hipError_t e = hipSuccess;
-        switch (pl.lpr) {
-            case 8: e = launch_lpr<MODE, F16IN, 8>(pl.nch, p, grid, lds, stream); break;
-            case 16: e = launch_lpr<MODE, F16IN, 16>(pl.nch, p, grid, lds, stream); break;
-            case 32: e = launch_lpr<MODE, F16IN, 32>(pl.nch, p, grid, lds, stream); break;
-            default: e = launch_lpr<MODE, F16IN, 64>(pl.nch, p, grid, lds, stream); break;
-        }
-        if (e != hipSuccess) return fail(QE_ERR_UNSUPPORTED, "%s: no kernel for K=%d", what, K);
+    Plan pl{};
+    if (KC <= 16 * 6) {
+        pl.lpr = 16;
+        const int n = (KC + 15) / 16;
+        pl.nch = n <= 2 ? 2 : (n <= 3 ? 3 : 6);
     } else {
-        if (K > kMaxGenericK) return fail(QE_ERR_UNSUPPORTED, "%s: in_features=%d exceeds %d", what, K, kMaxGenericK);
-        int grid = (p.n_out + 3) / 4;
-        if (grid > max_grid) grid = max_grid;
-        const size_t lds = static_cast<size_t>(K) + K / 2 + K / 32;
-        gemv_w4_generic_kernel<MODE, F16IN><<<grid, 256, lds, stream>>>(p);
+        pl.lpr = 64;
+        const int n = (KC + 63) / 64;
+        pl.nch = n <= 3 ? 3 : (n <= 5 ? 5 : 8);
     }
+    pl.rps = (mode == kSwiglu || n_rows >= 4096) ? 2 : 1;
+    (void)f16_input;
+    const int sets = (n_rows + pl.rps - 1) / pl.rps;
+    const int blocks256 = (sets + (256 / pl.lpr) - 1) / (256 / pl.lpr);
+    pl.bt = blocks256 >= 4 * cu_count() ? 256 : 64;
+    return pl;
+}
+
+template <int MODE, int XM, int BT, int LPR, int NCH, int RPS>
+void launch_fast(const GemvParams& p, hipStream_t s) {
+    constexpr int SEGS = BT / LPR;
+    const int sets = (p.n_rows + RPS - 1) / RPS;
+    int grid = (sets + SEGS - 1) / SEGS;
+    const int cap = cu_count() * (BT == 256 ? 4 : 8);
+    if (grid > cap) grid = cap;
+    const size_t lds = XM == kXQ8 ? 0 : static_cast<size_t>(p.K) + (p.K >> 5) * 8;
+    gemv_w4_kernel<BT, LPR, NCH, RPS, MODE, XM><<<grid, BT, lds, s>>>(p);
+}
+
+template <int MODE, int XM, int BT, int RPS>
+bool dispatch_chunks(const Plan& pl, const GemvParams& p, hipStream_t s) {
+    if (pl.lpr == 16) {
+        switch (pl.nch) {
+            case 2: launch_fast<MODE, XM, BT, 16, 2, RPS>(p, s); return true;
+            case 3: launch_fast<MODE, XM, BT, 16, 3, RPS>(p, s); return true;
+            case 6: launch_fast<MODE, XM, BT, 16, 6, RPS>(p, s); return true;
+        }
+    } else {
+        switch (pl.nch) {
+            case 3: launch_fast<MODE, XM, BT, 64, 3, RPS>(p, s); return true;
+            case 5: launch_fast<MODE, XM, BT, 64, 5, RPS>(p, s); return true;
+            case 8: launch_fast<MODE, XM, BT, 64, 8, RPS>(p, s); return true;
+        }
+    }
+    return false;
+}
+
+template <int MODE, int XM>
+bool dispatch_fast(const Plan& pl, const GemvParams& p, hipStream_t s) {
+    if constexpr (XM != kXQ8) {  // fp16 activations are staged by 256-thread blocks
+        if constexpr (MODE == kSwiglu) {
+            return dispatch_chunks<MODE, XM, 256, 2>(pl, p, s);
+        } else {
+            return pl.rps == 2 ? dispatch_chunks<MODE, XM, 256, 2>(pl, p, s)
+                               : dispatch_chunks<MODE, XM, 256, 1>(pl, p, s);
+        }
+    } else if constexpr (MODE == kSwiglu) {
+        return pl.bt == 256 ? dispatch_chunks<MODE, XM, 256, 2>(pl, p, s) : dispatch_chunks<MODE, XM, 64, 2>(pl, p, s);
+    } else {
+        if (pl.rps == 2)
+            return pl.bt == 256 ? dispatch_chunks<MODE, XM, 256, 2>(pl, p, s)
+                                : dispatch_chunks<MODE, XM, 64, 2>(pl, p, s);
+        return pl.bt == 256 ? dispatch_chunks<MODE, XM, 256, 1>(pl, p, s) : dispatch_chunks<MODE, XM, 64, 1>(pl, p, s);
+    }
+}
+
+template <int MODE, int XM>
+int launch_gemv(GemvParams& p, bool fast_ok, hipStream_t stream, const char* what) {
+    const int K = p.K;
+    if (p.n_rows <= 0) return QE_OK;
+    if (fast_ok && K <= kMaxFastK) {
+        const Plan pl = plan_for(K, p.n_rows, MODE, XM != kXQ8);
+        bool qkv_ok = true;
+        if (MODE == kQKV && pl.rps == 2) qkv_ok = (p.row_begin[1] % 2 == 0) && (p.row_begin[2] % 2 == 0);
+        if (qkv_ok) {
+            if (!dispatch_fast<MODE, XM>(pl, p, stream))
+                return fail(QE_ERR_UNSUPPORTED, "%s: no kernel for K=%d", what, K);
+            return check_launch(what);
+        }
+    }
+    if (K > kMaxGenericK) return fail(QE_ERR_UNSUPPORTED, "%s: in_features=%d exceeds %d", what, K, kMaxGenericK);
+    const int n_out = (MODE == kSwiglu) ? p.n_rows / 2 : p.n_rows;
+    int grid = (n_out + 3) / 4;
+    if (grid > cu_count() * 8) grid = cu_count() * 8;
+    const size_t lds = static_cast<size_t>(K) + (K >> 5) * 8;
+    gemv_w4_generic_kernel<MODE, XM><<<grid, 256, lds, stream>>>(p);
     return check_launch(what);
 }
 
-int check_common(const char* what, int K, const void* q8, const void* xs, const void* s8, const void* x16) {
+int check_k(const char* what, int K) {
     QE_REQUIRE(K > 0 && K % 128 == 0, "%s: in_features=%d must be a positive multiple of 128", what, K);
-    if (x16 == nullptr) QE_REQUIRE(q8 && xs && s8, "%s: Q8_1 input pointers must not be NULL", what);
     return QE_OK;
 }
 
 bool act_fast_ok(const GemvParams& p) {
-    if (p.x16) return aligned(p.x16, 16);
+    if (p.x16)
+        return aligned(p.x16, 16) && (p.gamma == nullptr || aligned(p.gamma, 16)) &&
+               (p.norm_out == nullptr || aligned(p.norm_out, 16));
     return aligned(p.q8, 16) && aligned(p.s8, 16);
 }
 
-}  // namespace
-}  // namespace qe
-
-using namespace qe;
-
-extern "C" int qe_launch_gemv_w4a8(const uint32_t* qweight, const uint16_t* scales, const int8_t* input_q8,
-                                   const float* input_scale, const int32_t* input_sum8, const uint16_t* residual,
-                                   uint16_t* output_y, int out_features, int in_features, hipStream_t stream) {
-    const char* what = "gemv_w4a8";
-    if (int rc = check_common(what, in_features, input_q8, input_scale, input_sum8, nullptr)) return rc;
-    QE_REQUIRE(qweight && scales && output_y, "%s: NULL weight/scale/output", what);
-    QE_REQUIRE(out_features >= 0, "%s: out_features=%d", what, out_features);
-    QE_REQUIRE(aligned(qweight, 4) && aligned(scales, 2), "%s: weights must be 4-byte aligned", what);
-    GemvParams p{};
-    p.qw[0] = qweight;
-    p.sc[0] = scales;
-    p.out[0] = output_y;
-    p.residual = residual;
-    p.q8 = input_q8;
-    p.xs = input_scale;
-    p.s8 = input_sum8;
-    p.n_out = out_features;
-    p.K = in_features;
-    const bool fast = aligned(qweight, 16) && act_fast_ok(p);
-    return launch_gemv<kPlain, false>(p, fast, stream, what);
-}
-
-extern "C" int qe_launch_gemv_qkv_w4a8(const qe_qkv_view* view, const int8_t* input_q8, const float* input_scale,
-                                       const int32_t* input_sum8, hipStream_t stream, int in_features,
-                                       int num_q_heads, int num_kv_heads, int head_dim) {
-    const char* what = "gemv_qkv_w4a8";
-    if (int rc = check_common(what, in_features, input_q8, input_scale, input_sum8, nullptr)) return rc;
+int fill_qkv(GemvParams& p, const qe_qkv_view* view, int num_q_heads, int num_kv_heads, int head_dim, bool& fast,
+             const char* what) {
     QE_REQUIRE(view != nullptr, "%s: view is NULL", what);
     QE_REQUIRE(num_q_heads >= 0 && num_kv_heads >= 0 && head_dim >= 0, "%s: negative head shape", what);
     const int q_dim = num_q_heads * head_dim;
@@ -350,8 +556,7 @@ extern "C" int qe_launch_gemv_qkv_w4a8(const qe_qkv_view* view, const int8_t* in
     const uint16_t* s[3] = {view->q_scale, view->k_scale, view->v_scale};
     uint16_t* o[3] = {view->d_q, view->d_k, view->d_v};
     const int rows[3] = {q_dim, kv_dim, kv_dim};
-    bool fast = true;
-    GemvParams p{};
+    fast = true;
     for (int i = 0; i < 3; ++i) {
         if (rows[i] == 0) continue;
         QE_REQUIRE(w[i] && s[i] && o[i], "%s: NULL pointer in view (matrix %d)", what, i);
@@ -364,13 +569,51 @@ extern "C" int qe_launch_gemv_qkv_w4a8(const qe_qkv_view* view, const int8_t* in
     p.row_begin[0] = 0;
     p.row_begin[1] = q_dim;
     p.row_begin[2] = q_dim + kv_dim;
+    p.n_rows = q_dim + 2 * kv_dim;
+    return QE_OK;
+}
+
+}  // namespace
+}  // namespace qe
+
+using namespace qe;
+
+extern "C" int qe_launch_gemv_w4a8(const uint32_t* qweight, const uint16_t* scales, const int8_t* input_q8,
+                                   const float* input_scale, const int32_t* input_sum8, const uint16_t* residual,
+                                   uint16_t* output_y, int out_features, int in_features, hipStream_t stream) {
+    const char* what = "gemv_w4a8";
+    if (int rc = check_k(what, in_features)) return rc;
+    QE_REQUIRE(input_q8 && input_scale && input_sum8, "%s: Q8_1 input pointers must not be NULL", what);
+    QE_REQUIRE(qweight && scales && output_y, "%s: NULL weight/scale/output", what);
+    QE_REQUIRE(out_features >= 0, "%s: out_features=%d", what, out_features);
+    QE_REQUIRE(aligned(qweight, 4) && aligned(scales, 2), "%s: weights must be 4-byte aligned", what);
+    GemvParams p{};
+    p.qw[0] = qweight;
+    p.sc[0] = scales;
+    p.out[0] = output_y;
+    p.residual = residual;
     p.q8 = input_q8;
     p.xs = input_scale;
     p.s8 = input_sum8;
-    p.n_out = q_dim + 2 * kv_dim;
+    p.n_rows = out_features;
     p.K = in_features;
-    fast = fast && act_fast_ok(p);
-    return launch_gemv<kQKV, false>(p, fast, stream, what);
+    return launch_gemv<kPlain, kXQ8>(p, aligned(qweight, 16) && act_fast_ok(p), stream, what);
+}
+
+extern "C" int qe_launch_gemv_qkv_w4a8(const qe_qkv_view* view, const int8_t* input_q8, const float* input_scale,
+                                       const int32_t* input_sum8, hipStream_t stream, int in_features,
+                                       int num_q_heads, int num_kv_heads, int head_dim) {
+    const char* what = "gemv_qkv_w4a8";
+    if (int rc = check_k(what, in_features)) return rc;
+    QE_REQUIRE(input_q8 && input_scale && input_sum8, "%s: Q8_1 input pointers must not be NULL", what);
+    GemvParams p{};
+    bool fast = true;
+    if (int rc = fill_qkv(p, view, num_q_heads, num_kv_heads, head_dim, fast, what)) return rc;
+    p.q8 = input_q8;
+    p.xs = input_scale;
+    p.s8 = input_sum8;
+    p.K = in_features;
+    return launch_gemv<kQKV, kXQ8>(p, fast && act_fast_ok(p), stream, what);
 }
 
 extern "C" int qe_launch_gemv_dual_gate_up_swiglu_w4a8(const uint32_t* gate_up_qweight, const uint16_t* gate_up_scales,
@@ -378,7 +621,8 @@ extern "C" int qe_launch_gemv_dual_gate_up_swiglu_w4a8(const uint32_t* gate_up_q
                                                        const int32_t* input_sum8, uint16_t* output_mlp,
                                                        int hidden_size, int intermediate_size, hipStream_t stream) {
     const char* what = "gemv_dual_gate_up_swiglu_w4a8";
-    if (int rc = check_common(what, hidden_size, input_q8, input_scale, input_sum8, nullptr)) return rc;
+    if (int rc = check_k(what, hidden_size)) return rc;
+    QE_REQUIRE(input_q8 && input_scale && input_sum8, "%s: Q8_1 input pointers must not be NULL", what);
     QE_REQUIRE(gate_up_qweight && gate_up_scales && output_mlp, "%s: NULL weight/scale/output", what);
     QE_REQUIRE(intermediate_size >= 0, "%s: intermediate_size=%d", what, intermediate_size);
     QE_REQUIRE(aligned(gate_up_qweight, 4) && aligned(gate_up_scales, 2), "%s: weights must be 4-byte aligned", what);
@@ -389,17 +633,16 @@ extern "C" int qe_launch_gemv_dual_gate_up_swiglu_w4a8(const uint32_t* gate_up_q
     p.q8 = input_q8;
     p.xs = input_scale;
     p.s8 = input_sum8;
-    p.n_out = intermediate_size;
+    p.n_rows = 2 * intermediate_size;
     p.K = hidden_size;
-    const bool fast = aligned(gate_up_qweight, 16) && act_fast_ok(p);
-    return launch_gemv<kSwiglu, false>(p, fast, stream, what);
+    return launch_gemv<kSwiglu, kXQ8>(p, aligned(gate_up_qweight, 16) && act_fast_ok(p), stream, what);
 }
 
 extern "C" int qe_launch_gemv_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* input_x,
                                     const uint16_t* residual, uint16_t* output_y, int out_features, int in_features,
                                     hipStream_t stream) {
     const char* what = "gemv_w4a16";
-    if (int rc = check_common(what, in_features, nullptr, nullptr, nullptr, input_x)) return rc;
+    if (int rc = check_k(what, in_features)) return rc;
     QE_REQUIRE(input_x && qweight && scales && output_y, "%s: NULL pointer", what);
     QE_REQUIRE(out_features >= 0, "%s: out_features=%d", what, out_features);
     QE_REQUIRE(aligned(qweight, 4) && aligned(scales, 2) && aligned(input_x, 2), "%s: misaligned buffer", what);
@@ -409,10 +652,9 @@ extern "C" int qe_launch_gemv_w4a16(const uint32_t* qweight, const uint16_t* sca
     p.out[0] = output_y;
     p.residual = residual;
     p.x16 = input_x;
-    p.n_out = out_features;
+    p.n_rows = out_features;
     p.K = in_features;
-    const bool fast = aligned(qweight, 16) && act_fast_ok(p);
-    return launch_gemv<kPlain, true>(p, fast, stream, what);
+    return launch_gemv<kPlain, kXF16>(p, aligned(qweight, 16) && act_fast_ok(p), stream, what);
 }
 
 extern "C" int qe_launch_gemv_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_qweight,
@@ -420,7 +662,7 @@ extern "C" int qe_launch_gemv_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_
                                                         uint16_t* output_mlp, int hidden_size, int intermediate_size,
                                                         hipStream_t stream) {
     const char* what = "gemv_dual_gate_up_swiglu_w4a16";
-    if (int rc = check_common(what, hidden_size, nullptr, nullptr, nullptr, input_x)) return rc;
+    if (int rc = check_k(what, hidden_size)) return rc;
     QE_REQUIRE(input_x && gate_up_qweight && gate_up_scales && output_mlp, "%s: NULL pointer", what);
     QE_REQUIRE(intermediate_size >= 0, "%s: intermediate_size=%d", what, intermediate_size);
     QE_REQUIRE(aligned(gate_up_qweight, 4) && aligned(gate_up_scales, 2) && aligned(input_x, 2),
@@ -430,8 +672,50 @@ extern "C" int qe_launch_gemv_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_
     p.sc[0] = gate_up_scales;
     p.out[0] = output_mlp;
     p.x16 = input_x;
-    p.n_out = intermediate_size;
+    p.n_rows = 2 * intermediate_size;
     p.K = hidden_size;
-    const bool fast = aligned(gate_up_qweight, 16) && act_fast_ok(p);
-    return launch_gemv<kSwiglu, true>(p, fast, stream, what);
+    return launch_gemv<kSwiglu, kXF16>(p, aligned(gate_up_qweight, 16) && act_fast_ok(p), stream, what);
+}
+
+extern "C" int qe_launch_rmsnorm_gemv_qkv_w4a16(const uint16_t* input, const uint16_t* gamma,
+                                                uint16_t* output_fp16_opt, const qe_qkv_view* view,
+                                                hipStream_t stream, int hidden_size, int num_q_heads,
+                                                int num_kv_heads, int head_dim) {
+    const char* what = "rmsnorm_gemv_qkv_w4a16";
+    if (int rc = check_k(what, hidden_size)) return rc;
+    QE_REQUIRE(input && gamma, "%s: input/gamma is NULL", what);
+    QE_REQUIRE(aligned(input, 2) && aligned(gamma, 2) && aligned(output_fp16_opt, 2), "%s: misaligned buffer", what);
+    GemvParams p{};
+    bool fast = true;
+    if (int rc = fill_qkv(p, view, num_q_heads, num_kv_heads, head_dim, fast, what)) return rc;
+    p.x16 = input;
+    p.gamma = gamma;
+    p.norm_out = output_fp16_opt;
+    p.K = hidden_size;
+    return launch_gemv<kQKV, kXRMS>(p, fast && act_fast_ok(p), stream, what);
+}
+
+extern "C" int qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(const uint16_t* input, const uint16_t* gamma,
+                                                                uint16_t* output_fp16_opt,
+                                                                const uint32_t* gate_up_qweight,
+                                                                const uint16_t* gate_up_scales, uint16_t* output_mlp,
+                                                                int hidden_size, int intermediate_size,
+                                                                hipStream_t stream) {
+    const char* what = "rmsnorm_gemv_dual_gate_up_swiglu_w4a16";
+    if (int rc = check_k(what, hidden_size)) return rc;
+    QE_REQUIRE(input && gamma && gate_up_qweight && gate_up_scales && output_mlp, "%s: NULL pointer", what);
+    QE_REQUIRE(intermediate_size >= 0, "%s: intermediate_size=%d", what, intermediate_size);
+    QE_REQUIRE(aligned(gate_up_qweight, 4) && aligned(gate_up_scales, 2) && aligned(input, 2) && aligned(gamma, 2) &&
+                   aligned(output_fp16_opt, 2),
+               "%s: misaligned buffer", what);
+    GemvParams p{};
+    p.qw[0] = gate_up_qweight;
+    p.sc[0] = gate_up_scales;
+    p.out[0] = output_mlp;
+    p.x16 = input;
+    p.gamma = gamma;
+    p.norm_out = output_fp16_opt;
+    p.n_rows = 2 * intermediate_size;
+    p.K = hidden_size;
+    return launch_gemv<kSwiglu, kXRMS>(p, aligned(gate_up_qweight, 16) && act_fast_ok(p), stream, what);
 }

@@ -35,6 +35,8 @@ SIGNATURES = {
     "qe_launch_gemm_prefill_qkv_w4a16": [_P, _P, _I, _P, _I, _I, _I, _I, _I],
     "qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _I, _P, _I, _I],
     "qe_launch_sample_and_advance": [_P, _P, _P, _P, _P, _P, _I],
+    "qe_launch_rmsnorm_gemv_qkv_w4a16": [_P, _P, _P, _P, _P, _I, _I, _I, _I],
+    "qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _P, _P, _I, _I, _P],
 }
 
 _lib = None
@@ -167,3 +169,17 @@ def launch_sample_and_advance(logits, sample_scratch_val, sample_scratch_idx, d_
                               stream=None, vocab_size=151936):
     _call("qe_launch_sample_and_advance", _ptr(logits), _ptr(sample_scratch_val), _ptr(sample_scratch_idx),
           _ptr(d_control), _ptr(d_mapped_pinned_token), _stream(stream), vocab_size)
+
+
+# ---- fused decode entry points (no counterpart in the reference API) ---------
+def launch_rmsnorm_gemv_qkv_w4a16(input, gamma, output_fp16_opt, view: QKVView, stream=None, hidden_size=1536,
+                                  num_q_heads=12, num_kv_heads=2, head_dim=128):
+    _call("qe_launch_rmsnorm_gemv_qkv_w4a16", _ptr(input), _ptr(gamma), _ptr(output_fp16_opt),
+          ctypes.addressof(view), _stream(stream), hidden_size, num_q_heads, num_kv_heads, head_dim)
+
+
+def launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(input, gamma, output_fp16_opt, gate_up_qweight, gate_up_scales,
+                                                  output_mlp, hidden_size, intermediate_size, stream=None):
+    _call("qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16", _ptr(input), _ptr(gamma), _ptr(output_fp16_opt),
+          _ptr(gate_up_qweight), _ptr(gate_up_scales), _ptr(output_mlp), hidden_size, intermediate_size,
+          _stream(stream))

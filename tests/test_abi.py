@@ -1,0 +1,52 @@
+"""CPU checks of the C-ABI library: it loads, exports every entry point that
+include/qe_kernels.h declares, and rejects bad shapes before touching a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "qe_kernels.h")).read()
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(qe_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "qe_launch_gemv_w4a8" in names and "qe_last_error" in names
+    assert len(names) >= 16
+
+
+def test_library_exports_every_declared_symbol():
+    import qe_amd
+    L = qe_amd.lib()
+    for name in _declared():
+        assert hasattr(L, name), f"libqe_amd.so does not export {name}"
+    # and the Python binding covers every launcher
+    launchers = [n for n in _declared() if n.startswith("qe_launch_")]
+    assert sorted(launchers) == sorted(qe_amd.SIGNATURES)
+    assert qe_amd.lib().qe_version().decode().startswith("qe_amd")
+
+
+@pytest.mark.parametrize("K", [0, 100, 129, -128])
+def test_bad_k_rejected_on_host(K):
+    """Precondition checks run before any HIP call (no GPU needed)."""
+    import qe_amd
+    L = qe_amd.lib()
+    rc = L.qe_launch_gemv_w4a8(8, 8, 16, 16, 16, None, 16, 4, K, None)
+    assert rc == 1
+    assert "multiple of 128" in L.qe_last_error().decode()
+    rc = L.qe_launch_gemm_prefill_w4a16(16, 16, 16, None, 16, 4, 4, K, None, 0)
+    assert rc == 1
+
+
+def test_null_pointers_rejected_on_host():
+    import qe_amd
+    L = qe_amd.lib()
+    assert L.qe_launch_gemv_w4a8(None, None, None, None, None, None, None, 4, 128, None) == 1
+    assert L.qe_launch_quantize_fp16_to_q8_1(None, None, None, None, 128, None) == 1
+    assert L.qe_launch_gemv_qkv_w4a8(None, 16, 16, 16, None, 128, 1, 1, 128) == 1
+    assert "NULL" in L.qe_last_error().decode()

@@ -111,7 +111,8 @@ def test_gemv_swiglu_w4a8(qe, orc, I, K):
     assert_fp16_close(host(out), ex, bd, ref, what="swiglu w4a8")
 
 
-@pytest.mark.parametrize("N,K", [(8960, 1536), (1536, 8960), (64, 128), (333, 2560), (50, 20480)])
+@pytest.mark.parametrize("N,K", [(8960, 1536), (1536, 8960), (64, 128), (333, 2560), (50, 20480), (1001, 4096),
+                                 (7, 16384)])
 def test_gemv_w4a16(qe, orc, N, K):
     """W4A16 GEMV 1536->8960 with in-launch Q8_1 quantization."""
     print(f"gemv_w4a16 N={N} K={K}", flush=True)
@@ -160,3 +161,79 @@ def test_gemv_rejects_bad_k(qe):
     with pytest.raises(RuntimeError, match="multiple of 128"):
         qe.launch_gemv_w4a8(empty(10, torch.int32), empty(10, torch.float16), empty(100, torch.int8),
                             empty(1, torch.float32), empty(13, torch.int32), None, empty(4, torch.float16), 4, 100)
+
+
+@pytest.mark.parametrize("H", [1536, 256])
+def test_fused_rmsnorm_qkv(qe, orc, H):
+    """Fused RMSNorm + Q8_1 + QKV equals the reference's two-launch sequence
+    (rmsnorm_q8_1 then gemv_qkv_w4a8, src/engine.cu:367-379)."""
+    nq, nkv, hd = (12, 2, 128) if H == 1536 else (2, 1, 64)
+    dims = (nq * hd, nkv * hd, nkv * hd)
+    mats = [orc.synth_w4(600 + i, n, H) for i, n in enumerate(dims)]
+    x16 = (orc.synth_f16_normal(5, H).astype(np.float32) * 3).astype(np.float16)
+    g16 = (1 + 0.2 * orc.synth_f16_normal(6, H).astype(np.float32)).astype(np.float16)
+    dw = [(dev(w), dev(s)) for w, s in mats]
+    outs = [empty(n, torch.float16) for n in dims]
+    norm = empty(H, torch.float16)
+    view = qe.make_qkv_view(dw[0][0], dw[0][1], outs[0], dw[1][0], dw[1][1], outs[1], dw[2][0], dw[2][1], outs[2])
+    qe.launch_rmsnorm_gemv_qkv_w4a16(dev(x16), dev(g16), norm, view, hidden_size=H, num_q_heads=nq,
+                                     num_kv_heads=nkv, head_dim=hd)
+    fused = [host(o) for o in outs]
+    # two-launch path on the GPU
+    q8, sc, s8 = empty(H, torch.int8), empty(H // 128, torch.float32), empty(H // 8, torch.int32)
+    norm2 = empty(H, torch.float16)
+    qe.launch_rmsnorm_q8_1(dev(x16), dev(g16), norm2, q8, sc, s8, hidden_size=H)
+    outs2 = [empty(n, torch.float16) for n in dims]
+    view2 = qe.make_qkv_view(dw[0][0], dw[0][1], outs2[0], dw[1][0], dw[1][1], outs2[1], dw[2][0], dw[2][1], outs2[2])
+    qe.launch_gemv_qkv_w4a8(view2, q8, sc, s8, in_features=H, num_q_heads=nq, num_kv_heads=nkv, head_dim=hd)
+    n_gpu = host(norm)
+    from helpers import ulp16
+    # both kernels reduce the sum of squares in their own order: 1 ulp at most
+    assert np.all(np.abs(n_gpu.astype(np.float64) - host(norm2).astype(np.float64)) <= ulp16(n_gpu))
+    # oracle on the normalized vector the kernel produced
+    rq, rs, rs8 = orc.quantize_q8_1(n_gpu)
+    for (w, s), f, o2, n in zip(mats, fused, outs2, dims):
+        ref, ex, bd = orc.gemv_w4a8(w, s, rq, rs, rs8, n, H)
+        assert_fp16_close(f, ex, bd, ref, what="fused qkv")
+        assert_fp16_close(host(o2), ex, bd, ref, what="two-launch qkv")
+
+
+@pytest.mark.parametrize("H,I", [(1536, 8960), (256, 300)])
+def test_fused_rmsnorm_gate_up(qe, orc, H, I):
+    qw, sc = orc.synth_w4(700 + I, 2 * I, H)
+    x16 = (orc.synth_f16_normal(7, H).astype(np.float32) * 2).astype(np.float16)
+    g16 = (1 + 0.2 * orc.synth_f16_normal(8, H).astype(np.float32)).astype(np.float16)
+    out = empty(I, torch.float16)
+    norm = empty(H, torch.float16)
+    qe.launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(dev(x16), dev(g16), norm, dev(qw), dev(sc), out, H, I)
+    n_gpu = host(norm)
+    n_ref = orc.rmsnorm_fp16(x16, g16)
+    from helpers import ulp16
+    assert np.all(np.abs(n_gpu.astype(np.float64) - n_ref.astype(np.float64)) <= ulp16(n_ref))
+    ref, ex, bd = orc.gemv_swiglu_w4a16(qw, sc, n_gpu, H, I)
+    assert_fp16_close(host(out), ex, bd, ref, what="fused gate_up")
+
+
+def test_gemv_w4a16_residual_inplace_down(qe, orc):
+    """Down projection with the quantizer fused (W4A16 entry point) and the
+    residual in place, as the fused decode layer issues it."""
+    N, K = 1536, 8960
+    qw, sc = orc.synth_w4(800, N, K)
+    x = orc.synth_f16_normal(9, K)
+    res = orc.synth_f16_normal(10, N)
+    out = dev(res)
+    qe.launch_gemv_w4a16(dev(qw), dev(sc), dev(x), out, out, N, K)
+    ref, ex, bd = orc.gemv_w4a16(qw, sc, x, N, K, residual=res)
+    assert_fp16_close(host(out), ex, bd, ref, what="down w4a16 inplace")
+
+
+@pytest.mark.parametrize("N", [4096, 4097, 20000])
+def test_gemv_two_rows_per_segment_tails(qe, orc, N):
+    """Row counts >= 4096 use two rows per segment; odd counts exercise the
+    clamped tail row."""
+    K = 1536
+    qw, sc = orc.synth_w4(900 + N, N, K)
+    _, q8, xs, s8 = _act(orc, K, 13)
+    got = _gemv_w4a8(qe, qw, sc, q8, xs, s8, N, K)
+    ref, ex, bd = orc.gemv_w4a8(qw, sc, q8, xs, s8, N, K)
+    assert_fp16_close(got, ex, bd, ref, what=f"rps2 N={N}")
