@@ -1,0 +1,193 @@
+// kernels.hpp — C++20 host API of the W4A16 G128 matrix path, drop-in for
+// the reference's include/kernels.cuh launchers (namespace qwen, same names,
+// same argument order and defaults).  `cudaStream_t` becomes `hipStream_t`;
+// `half` is HIP's __half.  Every launcher forwards to the C-ABI in
+// qe_kernels.h and throws std::runtime_error on failure, as the reference's
+// CUDA_KERNEL_CHECK does (include/tensor.cuh:11-23).
+//
+// Only the launchers of the matrix path are declared here (plus greedy
+// sample_and_advance); embedding, RoPE and attention are outside this library.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "qe_kernels.h"
+
+namespace qwen {
+
+// Qwen2.5-1.5B dimensions, include/config.cuh:10-22.
+constexpr int32_t NUM_LAYERS = 28;
+constexpr int32_t HIDDEN_SIZE = 1536;
+constexpr int32_t INTERMEDIATE_SIZE = 8960;
+constexpr int32_t NUM_Q_HEADS = 12;
+constexpr int32_t NUM_KV_HEADS = 2;
+constexpr int32_t HEAD_DIM = 128;
+constexpr int32_t Q_DIM = 1536;
+constexpr int32_t KV_DIM = 256;
+constexpr int32_t VOCAB_SIZE = 151936;
+constexpr float RMS_NORM_EPS = 1e-6f;
+constexpr int32_t MAX_SEQ_LEN = 4096;
+constexpr int32_t QUANT_GROUP_SIZE = 128;
+
+// include/tensor.cuh:28-34
+using DeviceControlBlock = qe_device_control_block;
+static_assert(sizeof(DeviceControlBlock) == 256, "DeviceControlBlock layout");
+
+// include/kernels.cuh:23-27
+struct QKVProjectionView {
+    const void* q_weight; const half* q_scale; half* d_q;
+    const void* k_weight; const half* k_scale; half* d_k;
+    const void* v_weight; const half* v_scale; half* d_v;
+};
+static_assert(sizeof(QKVProjectionView) == sizeof(qe_qkv_view), "QKVProjectionView layout");
+
+namespace detail {
+inline void check(int rc, const char* what) {
+    if (rc != QE_OK) throw std::runtime_error(std::string(what) + ": " + qe_last_error());
+}
+inline const uint16_t* h(const half* p) { return reinterpret_cast<const uint16_t*>(p); }
+inline uint16_t* h(half* p) { return reinterpret_cast<uint16_t*>(p); }
+inline const qe_qkv_view* v(const QKVProjectionView& view) { return reinterpret_cast<const qe_qkv_view*>(&view); }
+}  // namespace detail
+
+// include/kernels.cuh:39-48
+inline void launch_rmsnorm_q8_1(const half* input, const half* gamma, half* output_fp16_opt, int8_t* out_q8,
+                                float* out_scale, int32_t* out_sum8, hipStream_t stream,
+                                int hidden_size = HIDDEN_SIZE) {
+    detail::check(qe_launch_rmsnorm_q8_1(detail::h(input), detail::h(gamma), detail::h(output_fp16_opt), out_q8,
+                                         out_scale, out_sum8, stream, hidden_size),
+                  "launch_rmsnorm_q8_1");
+}
+
+// include/kernels.cuh:30-37
+inline void launch_rmsnorm_fp16(const half* input, const half* gamma, half* output, int num_tokens,
+                                hipStream_t stream, int hidden_size = HIDDEN_SIZE) {
+    detail::check(qe_launch_rmsnorm_fp16(detail::h(input), detail::h(gamma), detail::h(output), num_tokens, stream,
+                                         hidden_size),
+                  "launch_rmsnorm_fp16");
+}
+
+// include/kernels.cuh:50-57
+inline void launch_quantize_fp16_to_q8_1(const half* input_x, int8_t* out_q8, float* out_scale, int32_t* out_sum8,
+                                         int num_elements, hipStream_t stream) {
+    detail::check(qe_launch_quantize_fp16_to_q8_1(detail::h(input_x), out_q8, out_scale, out_sum8, num_elements,
+                                                  stream),
+                  "launch_quantize_fp16_to_q8_1");
+}
+
+// include/kernels.cuh:60-69
+inline void launch_gemv_w4a16(const uint32_t* qweight, const half* scales, const half* input_x, const half* residual,
+                              half* output_y, int out_features, int in_features, hipStream_t stream) {
+    detail::check(qe_launch_gemv_w4a16(qweight, detail::h(scales), detail::h(input_x), detail::h(residual),
+                                       detail::h(output_y), out_features, in_features, stream),
+                  "launch_gemv_w4a16");
+}
+
+// include/kernels.cuh:71-82
+inline void launch_gemv_w4a8(const uint32_t* qweight, const half* scales, const int8_t* input_q8,
+                             const float* input_scale, const int32_t* input_sum8, const half* residual,
+                             half* output_y, int out_features, int in_features, hipStream_t stream) {
+    detail::check(qe_launch_gemv_w4a8(qweight, detail::h(scales), input_q8, input_scale, input_sum8,
+                                      detail::h(residual), detail::h(output_y), out_features, in_features, stream),
+                  "launch_gemv_w4a8");
+}
+
+// include/kernels.cuh:84-94
+inline void launch_gemv_qkv_w4a8(const QKVProjectionView& view, const int8_t* input_q8, const float* input_scale,
+                                 const int32_t* input_sum8, hipStream_t stream, int in_features = HIDDEN_SIZE,
+                                 int num_q_heads = NUM_Q_HEADS, int num_kv_heads = NUM_KV_HEADS,
+                                 int head_dim = HEAD_DIM) {
+    detail::check(qe_launch_gemv_qkv_w4a8(detail::v(view), input_q8, input_scale, input_sum8, stream, in_features,
+                                          num_q_heads, num_kv_heads, head_dim),
+                  "launch_gemv_qkv_w4a8");
+}
+
+// include/kernels.cuh:96-104
+inline void launch_gemv_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_qweight, const half* gate_up_scales,
+                                                  const half* input_x, half* output_mlp, int hidden_size,
+                                                  int intermediate_size, hipStream_t stream) {
+    detail::check(qe_launch_gemv_dual_gate_up_swiglu_w4a16(gate_up_qweight, detail::h(gate_up_scales),
+                                                           detail::h(input_x), detail::h(output_mlp), hidden_size,
+                                                           intermediate_size, stream),
+                  "launch_gemv_dual_gate_up_swiglu_w4a16");
+}
+
+// include/kernels.cuh:106-116
+inline void launch_gemv_dual_gate_up_swiglu_w4a8(const uint32_t* gate_up_qweight, const half* gate_up_scales,
+                                                 const int8_t* input_q8, const float* input_scale,
+                                                 const int32_t* input_sum8, half* output_mlp, int hidden_size,
+                                                 int intermediate_size, hipStream_t stream) {
+    detail::check(qe_launch_gemv_dual_gate_up_swiglu_w4a8(gate_up_qweight, detail::h(gate_up_scales), input_q8,
+                                                          input_scale, input_sum8, detail::h(output_mlp),
+                                                          hidden_size, intermediate_size, stream),
+                  "launch_gemv_dual_gate_up_swiglu_w4a8");
+}
+
+// include/kernels.cuh:119-130
+inline void launch_gemm_prefill_w4a16(const uint32_t* qweight, const half* scales, const half* input_x,
+                                      const half* residual, half* output_y, int M, int N, int K, hipStream_t stream,
+                                      int sm_count = 0) {
+    detail::check(qe_launch_gemm_prefill_w4a16(qweight, detail::h(scales), detail::h(input_x), detail::h(residual),
+                                               detail::h(output_y), M, N, K, stream, sm_count),
+                  "launch_gemm_prefill_w4a16");
+}
+
+// include/kernels.cuh:132-142
+inline void launch_gemm_prefill_qkv_w4a16(const QKVProjectionView& view, const half* input_x, int M,
+                                          hipStream_t stream, int in_features = HIDDEN_SIZE,
+                                          int num_q_heads = NUM_Q_HEADS, int num_kv_heads = NUM_KV_HEADS,
+                                          int head_dim = HEAD_DIM, int sm_count = 0) {
+    detail::check(qe_launch_gemm_prefill_qkv_w4a16(detail::v(view), detail::h(input_x), M, stream, in_features,
+                                                   num_q_heads, num_kv_heads, head_dim, sm_count),
+                  "launch_gemm_prefill_qkv_w4a16");
+}
+
+// include/kernels.cuh:144-153
+inline void launch_gemm_prefill_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_qweight,
+                                                          const half* gate_up_scales, const half* input_x,
+                                                          half* output_mlp, int M, hipStream_t stream,
+                                                          int hidden_size = HIDDEN_SIZE,
+                                                          int intermediate_size = INTERMEDIATE_SIZE) {
+    detail::check(qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(gate_up_qweight, detail::h(gate_up_scales),
+                                                                   detail::h(input_x), detail::h(output_mlp), M,
+                                                                   stream, hidden_size, intermediate_size),
+                  "launch_gemm_prefill_dual_gate_up_swiglu_w4a16");
+}
+
+// include/kernels.cuh:209-217 (greedy decoding)
+inline void launch_sample_and_advance(const half* logits, float* sample_scratch_val, int32_t* sample_scratch_idx,
+                                      DeviceControlBlock* d_control, int32_t* d_mapped_pinned_token,
+                                      hipStream_t stream, int vocab_size = VOCAB_SIZE) {
+    detail::check(qe_launch_sample_and_advance(detail::h(logits), sample_scratch_val, sample_scratch_idx, d_control,
+                                               d_mapped_pinned_token, stream, vocab_size),
+                  "launch_sample_and_advance");
+}
+
+// ---- fused decode launchers of this build (no counterpart in kernels.cuh) ----
+inline void launch_rmsnorm_gemv_qkv_w4a16(const half* input, const half* gamma, half* output_fp16_opt,
+                                          const QKVProjectionView& view, hipStream_t stream,
+                                          int hidden_size = HIDDEN_SIZE, int num_q_heads = NUM_Q_HEADS,
+                                          int num_kv_heads = NUM_KV_HEADS, int head_dim = HEAD_DIM) {
+    detail::check(qe_launch_rmsnorm_gemv_qkv_w4a16(detail::h(input), detail::h(gamma), detail::h(output_fp16_opt),
+                                                   detail::v(view), stream, hidden_size, num_q_heads, num_kv_heads,
+                                                   head_dim),
+                  "launch_rmsnorm_gemv_qkv_w4a16");
+}
+
+inline void launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(const half* input, const half* gamma,
+                                                          half* output_fp16_opt, const uint32_t* gate_up_qweight,
+                                                          const half* gate_up_scales, half* output_mlp,
+                                                          int hidden_size, int intermediate_size,
+                                                          hipStream_t stream) {
+    detail::check(qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(
+                      detail::h(input), detail::h(gamma), detail::h(output_fp16_opt), gate_up_qweight,
+                      detail::h(gate_up_scales), detail::h(output_mlp), hidden_size, intermediate_size, stream),
+                  "launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16");
+}
+
+}  // namespace qwen

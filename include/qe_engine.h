@@ -1,0 +1,68 @@
+/*
+ * qe_engine.h — C-ABI of the minimal Qwen2.5-style decode engine built on the
+ * W4A16 G128 path.  Weights are random-initialized on the device in the
+ * packed .qwenbin layout (uint32 [N][K/8] nibbles, fp16 [N][K/128] scales);
+ * the LM head is tied to the embedding.  One engine = one HIP stream, one
+ * device arena (allocated at create), one captured decode graph.
+ *
+ * Counterpart of the reference's QwenEngine (include/engine.cuh:104-226):
+ * prefill (:prefill), decode_step (:decode_step) and profile_stages.
+ * Session leasing, rollback, prefix reuse and the .qwenbin loader are not
+ * part of this build.
+ */
+#ifndef QE_ENGINE_H
+#define QE_ENGINE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct qe_engine qe_engine;
+
+typedef struct qe_engine_config {
+    int num_layers;         /* 28 */
+    int hidden_size;        /* 1536 */
+    int intermediate_size;  /* 8960 */
+    int num_q_heads;        /* 12 */
+    int num_kv_heads;       /* 2 */
+    int head_dim;           /* 128 (the only value built) */
+    int vocab_size;         /* 151936 */
+    int max_seq_len;        /* 4096 */
+    float rope_theta;       /* 1e6 */
+    int prefill_chunk;      /* tokens per prefill chunk */
+    int fused_decode;       /* 1: fused RMSNorm/quantize launches, 0: reference launch sequence */
+} qe_engine_config;
+
+/* Qwen2.5-1.5B dimensions. */
+void qe_engine_default_config(qe_engine_config* cfg);
+
+/* Allocate, random-initialize (seeded) and capture the decode graph. */
+int qe_engine_create(const qe_engine_config* cfg, uint64_t seed, qe_engine** out);
+void qe_engine_destroy(qe_engine* e);
+
+/* Position 0, token 0 (the KV cache is overwritten as positions advance). */
+int qe_engine_reset(qe_engine* e);
+
+/* Prefill n host tokens from position 0; *first_token receives the greedy
+ * next token.  Fails if n >= max_seq_len. */
+int qe_engine_prefill(qe_engine* e, const int32_t* tokens, int n, int32_t* first_token);
+
+/* n greedy decode steps (graph replay when use_graph != 0, else eager
+ * launches).  tokens[i] and step_ms[i] (hipEvent time of step i) are
+ * optional host arrays. */
+int qe_engine_decode(qe_engine* e, int n_steps, int use_graph, int32_t* tokens, float* step_ms);
+
+/* One eager decode step with events between launches: stage_ms[0] GEMV
+ * (projections + LM head), [1] attention, [2] other, [3] total. */
+int qe_engine_profile_decode(qe_engine* e, float* stage_ms);
+
+/* Next position to be written (tokens processed so far). */
+int qe_engine_seq_pos(const qe_engine* e);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -151,14 +151,57 @@ int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_qwe
 /* ---- greedy sampling ------------------------------------------------------ */
 
 /* Replaces launch_sample_and_advance, include/kernels.cuh:209-217, for
- * greedy decoding (temperature <= 1e-5): argmax with the lowest index on
- * ties, then token_id/seq_pos/rng_seed advance as the reference does.
- * sample_scratch_val/idx hold >= 256 entries.  A control block with
- * temperature > 1e-5 is rejected when it can be seen from the host
- * (it lives in device memory, so the kernel itself falls back to greedy). */
+ * greedy decoding: argmax over fp16 logits with the lowest index on ties
+ * (NaN never wins), then token_id = winner, seq_pos += 1, rng_seed += the
+ * reference's golden-ratio step.  sample_scratch_val/idx hold >= 256
+ * entries.  The control block's temperature is ignored: Gumbel sampling is
+ * not part of this build. */
 int qe_launch_sample_and_advance(const uint16_t* logits, float* sample_scratch_val,
                                  int32_t* sample_scratch_idx, qe_device_control_block* d_control,
                                  int32_t* d_mapped_pinned_token, hipStream_t stream, int vocab_size);
+
+/* ---- decode-loop kernels around the matrix path ---------------------------- */
+
+/* Replaces launch_embed_lookup_w4a16, include/kernels.cuh:11-20.  Token ids
+ * from d_token_ids, else d_control->token_id; ids outside [0, 151936) read
+ * row 0.  Rows are dequantized exactly as unpack_w4_to_half2_quad. */
+int qe_launch_embed_lookup_w4a16(const uint32_t* embed_qweight, const uint16_t* embed_scales,
+                                 const int32_t* d_token_ids, uint16_t* out_hidden,
+                                 const qe_device_control_block* d_control, int num_tokens, hipStream_t stream,
+                                 int hidden_size);
+
+/* Replaces launch_qkv_bias_rope_kv_append, include/kernels.cuh:156-174. */
+int qe_launch_qkv_bias_rope_kv_append(uint16_t* q, uint16_t* k, uint16_t* v, const uint16_t* q_bias,
+                                      const uint16_t* k_bias, const uint16_t* v_bias, uint16_t* layer_k_cache,
+                                      uint16_t* layer_v_cache, const qe_device_control_block* d_control,
+                                      int num_tokens, hipStream_t stream, int num_q_heads, int num_kv_heads,
+                                      int head_dim, int max_seq_len, int rotary_dim, float rope_theta);
+
+/* Replaces launch_attention_gqa_flash_decode, include/kernels.cuh:177-193
+ * (16 splits; head_dim 128).  With out_q8 != NULL the combine stage also
+ * writes the Q8_1 of the attention output (one group per head): d =
+ * max(max|acc|/127, 1e-8), q = clamp(rint(acc / d)), as
+ * src/kernels/attention_gqa.cu:263-310. */
+int qe_launch_attention_gqa_flash_decode(const uint16_t* q, const uint16_t* layer_k_cache,
+                                         const uint16_t* layer_v_cache, float* splitk_partial_out,
+                                         float* splitk_partial_lse, uint16_t* attn_out,
+                                         const qe_device_control_block* d_control, hipStream_t stream,
+                                         int num_q_heads, int num_kv_heads, int head_dim, int max_seq_len,
+                                         int8_t* out_q8, float* out_scale, int32_t* out_sum8);
+
+/* The combine stage alone (stage 2 of the flash decode plus the Q8_1
+ * epilogue), over caller-provided split partials [head][16][128] and
+ * (max, denominator) pairs [head][16][2].  No counterpart in the reference
+ * API (the reference launches it only inside flash_decode). */
+int qe_launch_attention_gqa_flash_decode_combine(const float* splitk_partial_out, const float* splitk_partial_lse,
+                                                 uint16_t* attn_out, hipStream_t stream, int num_q_heads,
+                                                 int8_t* out_q8, float* out_scale, int32_t* out_sum8);
+
+/* Replaces launch_attention_gqa_prefill, include/kernels.cuh:195-207. */
+int qe_launch_attention_gqa_prefill(const uint16_t* q, const uint16_t* layer_k_cache, const uint16_t* layer_v_cache,
+                                    uint16_t* attn_out, const qe_device_control_block* d_control, int num_tokens,
+                                    hipStream_t stream, int num_q_heads, int num_kv_heads, int head_dim,
+                                    int max_seq_len, int hidden_size);
 
 #ifdef __cplusplus
 }

@@ -37,6 +37,21 @@ SIGNATURES = {
     "qe_launch_sample_and_advance": [_P, _P, _P, _P, _P, _P, _I],
     "qe_launch_rmsnorm_gemv_qkv_w4a16": [_P, _P, _P, _P, _P, _I, _I, _I, _I],
     "qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _P, _P, _I, _I, _P],
+    "qe_launch_embed_lookup_w4a16": [_P, _P, _P, _P, _P, _I, _P, _I],
+    "qe_launch_qkv_bias_rope_kv_append": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I,
+                                          ctypes.c_float],
+    "qe_launch_attention_gqa_flash_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P],
+    "qe_launch_attention_gqa_flash_decode_combine": [_P, _P, _P, _P, _I, _P, _P, _P],
+    "qe_launch_attention_gqa_prefill": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I],
+}
+
+ENGINE_SIGNATURES = {
+    "qe_engine_create": [_P, ctypes.c_uint64, _P],
+    "qe_engine_reset": [_P],
+    "qe_engine_prefill": [_P, _P, _I, _P],
+    "qe_engine_decode": [_P, _I, _I, _P, _P],
+    "qe_engine_profile_decode": [_P, _P],
+    "qe_engine_seq_pos": [_P],
 }
 
 _lib = None
@@ -64,6 +79,14 @@ def lib():
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = ctypes.c_int
+        for name, args in ENGINE_SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        L.qe_engine_destroy.argtypes = [_P]
+        L.qe_engine_destroy.restype = None
+        L.qe_engine_default_config.argtypes = [_P]
+        L.qe_engine_default_config.restype = None
         L.qe_last_error.restype = ctypes.c_char_p
         L.qe_version.restype = ctypes.c_char_p
         _lib = L
@@ -183,3 +206,98 @@ def launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(input, gamma, output_fp16_opt,
     _call("qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16", _ptr(input), _ptr(gamma), _ptr(output_fp16_opt),
           _ptr(gate_up_qweight), _ptr(gate_up_scales), _ptr(output_mlp), hidden_size, intermediate_size,
           _stream(stream))
+
+
+# ---- decode-loop kernels ---------------------------------------------------------
+def launch_embed_lookup_w4a16(embed_qweight, embed_scales, d_token_ids, out_hidden, d_control, num_tokens,
+                              stream=None, hidden_size=1536):
+    _call("qe_launch_embed_lookup_w4a16", _ptr(embed_qweight), _ptr(embed_scales), _ptr(d_token_ids),
+          _ptr(out_hidden), _ptr(d_control), num_tokens, _stream(stream), hidden_size)
+
+
+def launch_qkv_bias_rope_kv_append(q, k, v, q_bias, k_bias, v_bias, layer_k_cache, layer_v_cache, d_control,
+                                   num_tokens, stream=None, num_q_heads=12, num_kv_heads=2, head_dim=128,
+                                   max_seq_len=4096, rotary_dim=0, rope_theta=1000000.0):
+    _call("qe_launch_qkv_bias_rope_kv_append", _ptr(q), _ptr(k), _ptr(v), _ptr(q_bias), _ptr(k_bias), _ptr(v_bias),
+          _ptr(layer_k_cache), _ptr(layer_v_cache), _ptr(d_control), num_tokens, _stream(stream), num_q_heads,
+          num_kv_heads, head_dim, max_seq_len, rotary_dim, rope_theta)
+
+
+def launch_attention_gqa_flash_decode(q, layer_k_cache, layer_v_cache, splitk_partial_out, splitk_partial_lse,
+                                      attn_out, d_control, stream=None, num_q_heads=12, num_kv_heads=2, head_dim=128,
+                                      max_seq_len=4096, out_q8=None, out_scale=None, out_sum8=None):
+    _call("qe_launch_attention_gqa_flash_decode", _ptr(q), _ptr(layer_k_cache), _ptr(layer_v_cache),
+          _ptr(splitk_partial_out), _ptr(splitk_partial_lse), _ptr(attn_out), _ptr(d_control), _stream(stream),
+          num_q_heads, num_kv_heads, head_dim, max_seq_len, _ptr(out_q8), _ptr(out_scale), _ptr(out_sum8))
+
+
+def launch_attention_gqa_flash_decode_combine(splitk_partial_out, splitk_partial_lse, attn_out, num_q_heads,
+                                              out_q8=None, out_scale=None, out_sum8=None, stream=None):
+    _call("qe_launch_attention_gqa_flash_decode_combine", _ptr(splitk_partial_out), _ptr(splitk_partial_lse),
+          _ptr(attn_out), _stream(stream), num_q_heads, _ptr(out_q8), _ptr(out_scale), _ptr(out_sum8))
+
+
+def launch_attention_gqa_prefill(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, stream=None,
+                                 num_q_heads=12, num_kv_heads=2, head_dim=128, max_seq_len=4096, hidden_size=1536):
+    _call("qe_launch_attention_gqa_prefill", _ptr(q), _ptr(layer_k_cache), _ptr(layer_v_cache), _ptr(attn_out),
+          _ptr(d_control), num_tokens, _stream(stream), num_q_heads, num_kv_heads, head_dim, max_seq_len,
+          hidden_size)
+
+
+# ---- engine ------------------------------------------------------------------------
+class EngineConfig(ctypes.Structure):
+    """qe_engine_config (include/qe_engine.h)."""
+    _fields_ = [("num_layers", _I), ("hidden_size", _I), ("intermediate_size", _I), ("num_q_heads", _I),
+                ("num_kv_heads", _I), ("head_dim", _I), ("vocab_size", _I), ("max_seq_len", _I),
+                ("rope_theta", ctypes.c_float), ("prefill_chunk", _I), ("fused_decode", _I)]
+
+
+def default_config() -> EngineConfig:
+    c = EngineConfig()
+    lib().qe_engine_default_config(ctypes.byref(c))
+    return c
+
+
+class Engine:
+    """Random-init Qwen2.5-style decode engine (include/qe_engine.h)."""
+
+    def __init__(self, cfg: EngineConfig | None = None, seed: int = 42):
+        self.cfg = cfg if cfg is not None else default_config()
+        h = ctypes.c_void_p()
+        _check(lib().qe_engine_create(ctypes.byref(self.cfg), seed, ctypes.byref(h)), "qe_engine_create")
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().qe_engine_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        _check(lib().qe_engine_reset(self._h), "qe_engine_reset")
+
+    def prefill(self, tokens) -> int:
+        arr = (ctypes.c_int32 * len(tokens))(*tokens)
+        out = ctypes.c_int32()
+        _check(lib().qe_engine_prefill(self._h, arr, len(tokens), ctypes.byref(out)), "qe_engine_prefill")
+        return out.value
+
+    def decode(self, n: int, use_graph: bool = True, timed: bool = False):
+        toks = (ctypes.c_int32 * max(n, 1))()
+        ms = (ctypes.c_float * max(n, 1))() if timed else None
+        _check(lib().qe_engine_decode(self._h, n, int(use_graph), toks, ms), "qe_engine_decode")
+        return (list(toks)[:n], list(ms)[:n]) if timed else list(toks)[:n]
+
+    def profile_decode(self):
+        st = (ctypes.c_float * 4)()
+        _check(lib().qe_engine_profile_decode(self._h, st), "qe_engine_profile_decode")
+        return {"gemv_ms": st[0], "attention_ms": st[1], "other_ms": st[2], "total_ms": st[3]}
+
+    @property
+    def seq_pos(self) -> int:
+        return lib().qe_engine_seq_pos(self._h)

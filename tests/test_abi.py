@@ -9,9 +9,9 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _declared():
-    text = open(os.path.join(ROOT, "include", "qe_kernels.h")).read()
-    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(qe_\w+)\s*\(", text, re.M)))
+def _declared(header="qe_kernels.h"):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    return sorted(set(re.findall(r"^(?:int|void|const char\*)\s+(qe_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_entry_points():
@@ -29,6 +29,8 @@ def test_library_exports_every_declared_symbol():
     launchers = [n for n in _declared() if n.startswith("qe_launch_")]
     assert sorted(launchers) == sorted(qe_amd.SIGNATURES)
     assert qe_amd.lib().qe_version().decode().startswith("qe_amd")
+    for name in _declared("qe_engine.h"):
+        assert hasattr(L, name), f"libqe_amd.so does not export {name}"
 
 
 @pytest.mark.parametrize("K", [0, 100, 129, -128])
@@ -50,3 +52,14 @@ def test_null_pointers_rejected_on_host():
     assert L.qe_launch_quantize_fp16_to_q8_1(None, None, None, None, 128, None) == 1
     assert L.qe_launch_gemv_qkv_w4a8(None, 16, 16, 16, None, 128, 1, 1, 128) == 1
     assert "NULL" in L.qe_last_error().decode()
+
+
+def test_engine_rejects_bad_config_on_host():
+    import ctypes
+    import qe_amd
+    c = qe_amd.default_config()
+    assert c.hidden_size == 1536 and c.num_layers == 28 and c.vocab_size == 151936
+    c.head_dim = 64
+    h = ctypes.c_void_p()
+    assert qe_amd.lib().qe_engine_create(ctypes.byref(c), 1, ctypes.byref(h)) == 1
+    assert "unsupported" in qe_amd.lib().qe_last_error().decode()

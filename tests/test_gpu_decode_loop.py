@@ -1,0 +1,212 @@
+"""GPU checks of the decode-loop kernels around the matrix path and of the
+engine built on it.
+
+* embedding: bit-exact against the oracle's W4 dequantization
+  (unpack_w4_to_half2_quad, quant_primitives.cuh:92-115);
+* flash-decode combine + Q8_1 epilogue (attention_gqa.cu:263-310): bit-exact
+  against the oracle when the combined value is exactly the partial (one
+  active split with denominator 1);
+* RoPE / flash decode / prefill attention: float kernels, checked against a
+  numpy float64 statement of the same math with a stated tolerance;
+* engine: graph replay and eager launches produce the same tokens
+  (tests/test_kernels.cu:635-684), same seed -> same tokens.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import dev, empty, host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def qe():
+    import qe_amd
+    qe_amd.lib()
+    return qe_amd
+
+
+def _ctl(seq_pos=0, token=0):
+    raw = np.zeros(64, np.int32)
+    raw[0], raw[1] = token, seq_pos
+    return dev(raw)
+
+
+def test_embed_lookup_bit_exact(qe, orc):
+    V, H = 1000, 1536
+    qw, sc = orc.synth_w4(31, V, H)
+    ids = np.array([0, 5, 999, 123, -1, 151936], np.int32)  # invalid ids read row 0
+    out = empty((len(ids), H), torch.float16)
+    qe.launch_embed_lookup_w4a16(dev(qw), dev(sc), dev(ids), out, None, len(ids), hidden_size=H)
+    got = host(out)
+    ref_rows = orc.dequant_w4_f16(qw, sc, V, H)
+    for i, t in enumerate(ids):
+        r = t if 0 <= t < V else 0
+        assert np.array_equal(got[i].view(np.uint16), ref_rows[r].view(np.uint16))
+    # token from the control block
+    out1 = empty((1, H), torch.float16)
+    qe.launch_embed_lookup_w4a16(dev(qw), dev(sc), None, out1, _ctl(token=777), 1, hidden_size=H)
+    assert np.array_equal(host(out1)[0].view(np.uint16), ref_rows[777].view(np.uint16))
+
+
+def test_flash_decode_combine_q8_epilogue_bit_exact(qe, orc):
+    nq, S, D = 12, 16, 128
+    rng = np.random.default_rng(3)
+    part = (rng.standard_normal((nq, S, D)) * rng.uniform(0.01, 50, (nq, 1, 1))).astype(np.float32)
+    part[3] = 0.0                                   # an all-zero head: d = 1e-8, q = 0
+    part[4, 0, :] = 0.0
+    part[4, 0, 0], part[4, 0, 1] = 127.0, 2.5       # rint tie: 2.5 -> 2 (half to even)
+    lse = np.zeros((nq, S, 2), np.float32)
+    lse[:, :, 0] = -np.inf
+    lse[:, 0, 0] = rng.standard_normal(nq).astype(np.float32)
+    lse[:, 0, 1] = 1.0                              # only split 0 active, denominator 1
+    out = empty(nq * D, torch.float16)
+    q8 = empty(nq * D, torch.int8)
+    sc = empty(nq, torch.float32)
+    s8 = empty(nq * D // 8, torch.int32)
+    qe.launch_attention_gqa_flash_decode_combine(dev(part), dev(lse), out, nq, q8, sc, s8)
+    acc = part[:, 0, :].reshape(-1)
+    r_out, r_q8, r_sc, r_s8 = orc.quantize_q8_1_attn(acc)
+    assert np.array_equal(host(out).view(np.uint16), r_out.view(np.uint16))
+    assert np.array_equal(host(q8), r_q8)
+    assert np.array_equal(host(sc).view(np.uint32), r_sc.view(np.uint32))
+    assert np.array_equal(host(s8), r_s8)
+    assert host(q8)[4 * D + 1] == 2
+
+
+def _attn_ref(q, kc, vc, seq_len, group):
+    nq, D = q.shape
+    out = np.zeros((nq, D))
+    for h in range(nq):
+        kvh = h // group
+        k = kc[kvh, :seq_len].astype(np.float64)
+        v = vc[kvh, :seq_len].astype(np.float64)
+        s = k @ q[h].astype(np.float64) / math.sqrt(D)
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ v
+    return out
+
+
+@pytest.mark.parametrize("seq_pos", [0, 5, 300, 4095])
+def test_flash_decode_attention(qe, orc, seq_pos):
+    nq, nkv, D, max_seq = 12, 2, 128, 4096
+    rng = np.random.default_rng(seq_pos)
+    q = rng.standard_normal((nq, D)).astype(np.float16)
+    kc = rng.standard_normal((nkv, max_seq, D)).astype(np.float16)
+    vc = rng.standard_normal((nkv, max_seq, D)).astype(np.float16)
+    part = empty(nq * 16 * D, torch.float32)
+    lse = empty(nq * 16 * 2, torch.float32)
+    out = empty(nq * D, torch.float16)
+    q8 = empty(nq * D, torch.int8)
+    sc = empty(nq, torch.float32)
+    s8 = empty(nq * D // 8, torch.int32)
+    qe.launch_attention_gqa_flash_decode(dev(q), dev(kc), dev(vc), part, lse, out, _ctl(seq_pos), num_q_heads=nq,
+                                         num_kv_heads=nkv, head_dim=D, max_seq_len=max_seq, out_q8=q8, out_scale=sc,
+                                         out_sum8=s8)
+    got = host(out).astype(np.float64).reshape(nq, D)
+    ref = _attn_ref(q, kc, vc, min(seq_pos + 1, max_seq), nq // nkv)
+    # fp32 online softmax vs float64: 2e-3 relative to the head's scale
+    assert np.all(np.abs(got - ref) <= 2e-3 * np.abs(ref).max(axis=1, keepdims=True) + 1e-3)
+    # Q8_1 epilogue consistent with the fp16 output: |q*d - out| <= d/2 (+ fp16 rounding)
+    d = host(sc).astype(np.float64)
+    qq = host(q8).astype(np.float64).reshape(nq, D)
+    assert np.all(np.abs(qq * d[:, None] - got) <= d[:, None] * 0.5 + 1e-3 * np.abs(got) + 1e-6)
+    assert np.array_equal(host(s8), -8 * host(q8).astype(np.int32).reshape(-1, 8).sum(1))
+
+
+def test_qkv_bias_rope_kv_append(qe):
+    nq, nkv, D, max_seq, T, base = 12, 2, 128, 512, 5, 37
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((T, nq * D)).astype(np.float16)
+    k = rng.standard_normal((T, nkv * D)).astype(np.float16)
+    v = rng.standard_normal((T, nkv * D)).astype(np.float16)
+    qb = (rng.standard_normal(nq * D) * 0.1).astype(np.float16)
+    kb = (rng.standard_normal(nkv * D) * 0.1).astype(np.float16)
+    vb = (rng.standard_normal(nkv * D) * 0.1).astype(np.float16)
+    dq, dk, dv = dev(q), dev(k), dev(v)
+    kc = torch.zeros((nkv, max_seq, D), dtype=torch.float16, device="cuda")
+    vc = torch.zeros((nkv, max_seq, D), dtype=torch.float16, device="cuda")
+    qe.launch_qkv_bias_rope_kv_append(dq, dk, dv, dev(qb), dev(kb), dev(vb), kc, vc, _ctl(base), T, num_q_heads=nq,
+                                      num_kv_heads=nkv, head_dim=D, max_seq_len=max_seq)
+
+    def rope(x, pos):  # x [heads, D] fp16 after bias
+        x = x.astype(np.float64)
+        i = np.arange(D // 2)
+        inv = np.exp2(-2.0 * i / D * math.log2(1e6))
+        a = pos * inv
+        x0, x1 = x[:, :D // 2], x[:, D // 2:]
+        return np.concatenate([x0 * np.cos(a) - x1 * np.sin(a), x0 * np.sin(a) + x1 * np.cos(a)], axis=1)
+
+    gq, gk, gkc, gvc = host(dq), host(dk), host(kc), host(vc)
+    for m in range(T):
+        qm = (q[m] + qb).astype(np.float16).reshape(nq, D)
+        km = (k[m] + kb).astype(np.float16).reshape(nkv, D)
+        vm = (v[m] + vb).astype(np.float16).reshape(nkv, D)
+        for got, ref in ((gq[m].reshape(nq, D), rope(qm, base + m)), (gk[m].reshape(nkv, D), rope(km, base + m))):
+            assert np.all(np.abs(got.astype(np.float64) - ref) <= 2e-3 * np.abs(ref) + 2e-3)
+        assert np.array_equal(gkc[:, base + m], gk[m].reshape(nkv, D))
+        assert np.array_equal(gvc[:, base + m], vm)
+    assert np.all(gkc[:, base + T:] == 0) and np.all(gkc[:, :base] == 0)
+
+
+@pytest.mark.parametrize("T,base", [(1, 0), (37, 0), (128, 0), (20, 100)])
+def test_prefill_attention(qe, T, base):
+    nq, nkv, D, max_seq = 12, 2, 128, 512
+    rng = np.random.default_rng(T + base)
+    q = rng.standard_normal((T, nq * D)).astype(np.float16)
+    kc = rng.standard_normal((nkv, max_seq, D)).astype(np.float16)
+    vc = rng.standard_normal((nkv, max_seq, D)).astype(np.float16)
+    out = empty((T, nq * D), torch.float16)
+    qe.launch_attention_gqa_prefill(dev(q), dev(kc), dev(vc), out, _ctl(base), T, num_q_heads=nq, num_kv_heads=nkv,
+                                    head_dim=D, max_seq_len=max_seq, hidden_size=nq * D)
+    got = host(out).astype(np.float64)
+    for m in range(T):
+        ref = _attn_ref(q[m].reshape(nq, D), kc, vc, base + m + 1, nq // nkv).reshape(-1)
+        assert np.all(np.abs(got[m] - ref) <= 2e-3 * np.abs(ref).max() + 1e-3)
+
+
+def _small_cfg(qe, fused=1):
+    c = qe.default_config()
+    c.num_layers, c.intermediate_size, c.vocab_size, c.max_seq_len, c.prefill_chunk = 2, 512, 4096, 256, 64
+    c.fused_decode = fused
+    return c
+
+
+def test_engine_graph_matches_eager_and_is_deterministic(qe):
+    prompt = [(i % 1000) + 100 for i in range(40)]  # the reference bench's synthetic prompt (cli_bench.cpp:78-82)
+    e = qe.Engine(_small_cfg(qe), seed=7)
+    t0 = e.prefill(prompt)
+    g = e.decode(12, use_graph=True)
+    assert e.seq_pos == len(prompt) + 12
+    e.reset()
+    assert e.prefill(prompt) == t0
+    eager = e.decode(12, use_graph=False)
+    assert g == eager
+    e2 = qe.Engine(_small_cfg(qe), seed=7)
+    assert e2.prefill(prompt) == t0 and e2.decode(12) == g
+    assert all(0 <= t < 4096 for t in g)
+    # the reference launch sequence computes the same integer stages: tokens agree
+    e3 = qe.Engine(_small_cfg(qe, fused=0), seed=7)
+    assert e3.prefill(prompt) == t0
+    ref_seq = e3.decode(12)
+    assert sum(a == b for a, b in zip(ref_seq, g)) >= 10
+    for x in (e, e2, e3):
+        x.close()
+
+
+def test_engine_context_limits(qe):
+    e = qe.Engine(_small_cfg(qe), seed=1)
+    with pytest.raises(RuntimeError, match="context window"):
+        e.prefill(list(range(256)))
+    with pytest.raises(RuntimeError, match="outside"):
+        e.prefill([5000])
+    e.prefill(list(range(250)))
+    e.decode(6)
+    with pytest.raises(RuntimeError, match="context window"):
+        e.decode(1)
+    prof_ok = e.seq_pos == 256
+    e.close()
+    assert prof_ok
