@@ -48,6 +48,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-step", action="store_true", help="headline step only (for profiling)")
+    ap.add_argument("--only-roofline", action="store_true", help="dominant kernel's timing only (for profiling)")
+    ap.add_argument("--calib-read", action="store_true",
+                    help="with --only-step: also stream-read 64 MiB 5 times (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (the W4A16 path has no multi-GPU "
@@ -111,6 +114,25 @@ def main():
     dk = torch.empty(NKV * HD, dtype=torch.float16, device=dev)
     dv = torch.empty(NKV * HD, dtype=torch.float16, device=dev)
     mlp = torch.empty(I, dtype=torch.float16, device=dev)
+
+    # per-kernel timing: a graph of back-to-back launches over rotating weight copies
+    def kernel_gbs(name, N, K, launch, nbytes, copies_bytes):
+        C = copies_for(copies_bytes)
+        qw, sc = rand_w4(N, K, C)
+        g = graph_of(lambda i: launch(qw[i % C], sc[i % C]), C)
+        ms = time_graph(g, 5) / C
+        return {"kernel": name, "us": round(ms * 1e3, 3), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+
+    if args.only_roofline:
+        # the dominant kernel's measurement alone (profiled by rocprofv3 for the committed summary)
+        qe_amd.launch_rmsnorm_q8_1(hidden, gamma, None, q8, xs, s8, hidden_size=H)
+        gu = kernel_gbs("rmsnorm_gemv_dual_gate_up_swiglu_w4a16 1536->2x8960", 2 * I, H,
+                        lambda w, s: qe_amd.launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(hidden, gamma, None, w, s,
+                                                                                         mlp, H, I),
+                        gemv_bytes(2 * I, H, act="f16", out_n=I) + H * 2, 2 * I * H // 2)
+        print(json.dumps({"roofline_kernel": gu}))
+        return
 
     # ---------------- headline: per-layer decode projection set --------------
     # Fused decode layer (this build's path, 4 launches):
@@ -199,18 +221,16 @@ def main():
         },
     }
     if args.only_step:
+        if args.calib_read:
+            buf = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+            sink = torch.zeros(1 << 14, dtype=torch.int32, device=dev)
+            for _ in range(5):
+                qe_amd.stream_read(buf, buf.numel(), sink)
+            torch.cuda.synchronize()
         print(json.dumps(result))
         return
 
     # ---------------- per-kernel GEMV roofline -------------------------------
-    def kernel_gbs(name, N, K, launch, nbytes, copies_bytes):
-        C = copies_for(copies_bytes)
-        qw, sc = rand_w4(N, K, C)
-        g = graph_of(lambda i: launch(qw[i % C], sc[i % C]), C)
-        ms = time_graph(g, 5) / C
-        return {"kernel": name, "us": round(ms * 1e3, 3), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nbytes}
-
     per = []
     qe_amd.launch_rmsnorm_q8_1(hidden, gamma, None, q8, xs, s8, hidden_size=H)
     torch.cuda.synchronize()
@@ -248,6 +268,23 @@ def main():
                     gemv_bytes(I, H, act="f16"), I * H // 2)
     per.append(c0)
 
+    # achievable ceiling: a launch that only streams the same number of bytes
+    sink = torch.zeros(1 << 14, dtype=torch.int32, device=dev)
+    ceil = {}
+    for nb in (gemv_bytes(H, H), b_gu_f, gemv_bytes(V, H), POOL_BYTES):
+        nb16 = (nb + 4095) // 4096 * 4096
+        C = copies_for(nb16) if nb16 < POOL_BYTES else 2
+        pool = torch.empty((C, nb16), dtype=torch.uint8, device=dev)
+        ms = time_graph(graph_of(lambda i: qe_amd.stream_read(pool[i % C], nb16, sink), C), 5) / C
+        ceil[str(nb)] = {"us": round(ms * 1e3, 3), "GB/s": round(nb16 / (ms * 1e-3) / 1e9, 1)}
+        del pool
+    result["stream_read_ceiling"] = ceil
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "gemv_gate_up_traffic.txt")
+    if os.path.exists(tfile):
+        for line in open(tfile):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = int(float(line.split(":", 1)[1]))
     result["roofline"] = {
         "kernel": gu["kernel"],
         "bound": "hbm",
@@ -255,8 +292,9 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": gu["frac"],
-        "traffic": None,
+        "traffic": traffic,
         "bytes_per_launch": b_gu_f,
+        "ceiling_same_bytes_GB/s": ceil[str(b_gu_f)]["GB/s"],
         "avg_launch_us": gu["us"],
     }
     result["kernels"] = per

@@ -61,6 +61,12 @@ int qe_engine_profile_decode(qe_engine* e, float* stage_ms);
 /* Next position to be written (tokens processed so far). */
 int qe_engine_seq_pos(const qe_engine* e);
 
+/* Device pointers of the last logits (fp16 [vocab]) and of the residual
+ * stream (fp16 [prefill_chunk][hidden]; row 0 after a decode step), for
+ * inspection after a synchronizing call. */
+const uint16_t* qe_engine_logits(const qe_engine* e);
+const uint16_t* qe_engine_hidden(const qe_engine* e);
+
 #ifdef __cplusplus
 }
 #endif

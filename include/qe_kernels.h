@@ -22,6 +22,7 @@
 #ifndef QE_KERNELS_H
 #define QE_KERNELS_H
 
+#include <stddef.h>
 #include <stdint.h>
 #include <hip/hip_runtime_api.h>
 
@@ -202,6 +203,14 @@ int qe_launch_attention_gqa_prefill(const uint16_t* q, const uint16_t* layer_k_c
                                     uint16_t* attn_out, const qe_device_control_block* d_control, int num_tokens,
                                     hipStream_t stream, int num_q_heads, int num_kv_heads, int head_dim,
                                     int max_seq_len, int hidden_size);
+
+/* ---- measurement ---------------------------------------------------------------- */
+
+/* Reads `bytes` from `data` with the GEMV weight-stream access pattern
+ * (16-byte nontemporal loads); `sink` receives nothing in practice (>= 16384
+ * uint32).  Used by bench.py for the streaming ceiling and to scale
+ * rocprofv3 FETCH_SIZE.  No counterpart in the reference. */
+int qe_stream_read(const void* data, size_t bytes, uint32_t* sink, hipStream_t stream);
 
 #ifdef __cplusplus
 }

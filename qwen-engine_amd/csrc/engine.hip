@@ -12,6 +12,7 @@
 // sequence is available with fused_decode = 0.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstring>
 #include <memory>
 #include <vector>
@@ -129,9 +130,14 @@ Mat alloc_mat(qe_engine* e, int rows, int K) {
     return m;
 }
 
-int init_mat(qe_engine* e, const Mat& m, uint64_t seed) {
+// Group scales |N(0,1)| * c with c = 1/sqrt(21.5 K): E[(q-8)^2] = 21.5 for
+// uniform nibbles, so a projection keeps the variance of its input and the
+// 28-layer residual stream stays inside fp16 (with c = 0.02 it overflows
+// after a few layers).  The embedding uses c = 0.02.
+int init_mat(qe_engine* e, const Mat& m, uint64_t seed, bool variance_preserving = true) {
+    const float c = variance_preserving ? 1.0f / sqrtf(21.5f * static_cast<float>(m.K)) : 0.02f;
     init_w4_kernel<<<2048, 256, 0, e->stream>>>(m.w, static_cast<size_t>(m.rows) * m.K / 8, m.s,
-                                                static_cast<size_t>(m.rows) * (m.K / 128), seed, 0.02f);
+                                                static_cast<size_t>(m.rows) * (m.K / 128), seed, c);
     QE_HIP(hipGetLastError());
     return QE_OK;
 }
@@ -376,7 +382,7 @@ extern "C" int qe_engine_create(const qe_engine_config* cfg, uint64_t seed, qe_e
         QE_TRY(init_vec(e.get(), L.k_bias, kvd, sd++, 0.0f, 0.02f));
         QE_TRY(init_vec(e.get(), L.v_bias, kvd, sd++, 0.0f, 0.02f));
     }
-    QE_TRY(init_mat(e.get(), e->embed, sd++));
+    QE_TRY(init_mat(e.get(), e->embed, sd++, false));
     QE_TRY(init_vec(e.get(), e->final_norm, H, sd++, 1.0f, 0.0f));
     (void)cu_count();  // cache the device fact before graph capture
     QE_HIP(hipMemsetAsync(e->kcache, 0, kvb, e->stream));
@@ -486,3 +492,7 @@ extern "C" int qe_engine_profile_decode(qe_engine* e, float* stage_ms) {
 }
 
 extern "C" int qe_engine_seq_pos(const qe_engine* e) { return e ? e->seq_pos : -1; }
+
+extern "C" const uint16_t* qe_engine_logits(const qe_engine* e) { return e ? e->logits : nullptr; }
+
+extern "C" const uint16_t* qe_engine_hidden(const qe_engine* e) { return e ? e->act0 : nullptr; }

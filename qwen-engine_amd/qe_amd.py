@@ -45,6 +45,10 @@ SIGNATURES = {
     "qe_launch_attention_gqa_prefill": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I],
 }
 
+OTHER_SIGNATURES = {
+    "qe_stream_read": [_P, ctypes.c_size_t, _P, _P],
+}
+
 ENGINE_SIGNATURES = {
     "qe_engine_create": [_P, ctypes.c_uint64, _P],
     "qe_engine_reset": [_P],
@@ -74,15 +78,22 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"libqe_amd.so not built at {LIB_PATH}; run __graft_entry__.build()")
+        # torch bundles its own libamdhip64 (same SONAME, libamdhip64.so.7).
+        # Loading torch first makes libqe_amd bind to that runtime, so the
+        # process has one HIP runtime and torch's streams/pointers are valid here.
+        import torch  # noqa: F401
         L = ctypes.CDLL(LIB_PATH)
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = ctypes.c_int
-        for name, args in ENGINE_SIGNATURES.items():
+        for name, args in list(ENGINE_SIGNATURES.items()) + list(OTHER_SIGNATURES.items()):
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = ctypes.c_int
+        for name in ("qe_engine_logits", "qe_engine_hidden"):
+            getattr(L, name).argtypes = [_P]
+            getattr(L, name).restype = ctypes.c_void_p
         L.qe_engine_destroy.argtypes = [_P]
         L.qe_engine_destroy.restype = None
         L.qe_engine_default_config.argtypes = [_P]
@@ -298,6 +309,34 @@ class Engine:
         _check(lib().qe_engine_profile_decode(self._h, st), "qe_engine_profile_decode")
         return {"gemv_ms": st[0], "attention_ms": st[1], "other_ms": st[2], "total_ms": st[3]}
 
+    def logits(self):
+        """Copy of the last logits (numpy float16)."""
+        return _device_f16(lib().qe_engine_logits(self._h), self.cfg.vocab_size)
+
+    def hidden_row0(self):
+        return _device_f16(lib().qe_engine_hidden(self._h), self.cfg.hidden_size)
+
     @property
     def seq_pos(self) -> int:
         return lib().qe_engine_seq_pos(self._h)
+
+
+def _device_f16(ptr: int, n: int):
+    import numpy as np
+    import torch
+    out = torch.empty(n, dtype=torch.float16, device="cuda")
+    torch.cuda.synchronize()
+    buf = (ctypes.c_char * (2 * n))
+    # device-to-device copy through HIP; torch has no wrapper for raw pointers
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [_P, _P, ctypes.c_size_t, _I]
+    rc = hip.hipMemcpy(out.data_ptr(), ptr, 2 * n, 3)  # hipMemcpyDeviceToDevice
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpy failed ({rc})")
+    del buf
+    return out.cpu().numpy()
+
+
+def stream_read(data, nbytes: int, sink, stream=None):
+    """Streaming-read kernel (qe_stream_read): bandwidth ceiling / counter calibration."""
+    _call("qe_stream_read", _ptr(data), nbytes, _ptr(sink), _stream(stream))

@@ -11,7 +11,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def _declared(header="qe_kernels.h"):
     text = open(os.path.join(ROOT, "include", header)).read()
-    return sorted(set(re.findall(r"^(?:int|void|const char\*)\s+(qe_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int|void|const char\*|const uint16_t\*)\s+(qe_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_entry_points():
@@ -63,3 +63,25 @@ def test_engine_rejects_bad_config_on_host():
     h = ctypes.c_void_p()
     assert qe_amd.lib().qe_engine_create(ctypes.byref(c), 1, ctypes.byref(h)) == 1
     assert "unsupported" in qe_amd.lib().qe_last_error().decode()
+
+
+def test_cpp_mirror_header_compiles(tmp_path):
+    """include/kernels.hpp (the reference-named C++ API) compiles against the C-ABI."""
+    import shutil
+    import subprocess
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    src = tmp_path / "use.cpp"
+    src.write_text(
+        '#include "kernels.hpp"\n'
+        "void f(const uint32_t* w, const half* s, const int8_t* q, const float* xs, const int32_t* s8,\n"
+        "       half* y, hipStream_t st) {\n"
+        "  qwen::launch_gemv_w4a8(w, s, q, xs, s8, y, y, qwen::HIDDEN_SIZE, qwen::Q_DIM, st);\n"
+        "  qwen::QKVProjectionView v{w, s, y, w, s, y, w, s, y};\n"
+        "  qwen::launch_gemv_qkv_w4a8(v, q, xs, s8, st);\n"
+        "  qwen::launch_gemm_prefill_dual_gate_up_swiglu_w4a16(w, s, y, y, 128, st);\n"
+        "}\n")
+    r = subprocess.run([hipcc, "-std=c++20", "-fsyntax-only", "-x", "hip", "--offload-arch=gfx950",
+                        f"-I{ROOT}/include", str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

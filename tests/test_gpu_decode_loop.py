@@ -188,6 +188,8 @@ def test_engine_graph_matches_eager_and_is_deterministic(qe):
     e2 = qe.Engine(_small_cfg(qe), seed=7)
     assert e2.prefill(prompt) == t0 and e2.decode(12) == g
     assert all(0 <= t < 4096 for t in g)
+    assert np.isfinite(e2.logits().astype(np.float32)).all()
+    assert np.isfinite(e2.hidden_row0().astype(np.float32)).all()
     # the reference launch sequence computes the same integer stages: tokens agree
     e3 = qe.Engine(_small_cfg(qe, fused=0), seed=7)
     assert e3.prefill(prompt) == t0
