@@ -62,10 +62,19 @@ int qe_engine_profile_decode(qe_engine* e, float* stage_ms);
 int qe_engine_seq_pos(const qe_engine* e);
 
 /* Device pointers of the last logits (fp16 [vocab]) and of the residual
- * stream (fp16 [prefill_chunk][hidden]; row 0 after a decode step), for
- * inspection after a synchronizing call. */
+ * stream (fp16 [prefill_chunk][hidden]; row 0 after a decode step). */
 const uint16_t* qe_engine_logits(const qe_engine* e);
 const uint16_t* qe_engine_hidden(const qe_engine* e);
+
+/* Synchronize the engine's stream and copy the first n fp16 values of the
+ * logits / residual stream to host memory. */
+int qe_engine_read_logits(qe_engine* e, uint16_t* host, int n);
+int qe_engine_read_hidden(qe_engine* e, uint16_t* host, int n);
+
+/* Synchronize and copy the first `bytes` of a named engine buffer to host
+ * memory: "logits", "hidden", "q8", "q8_scale", "q8_sum8", "embed_w",
+ * "embed_s", "final_norm", "control". */
+int qe_engine_read_buffer(qe_engine* e, const char* name, void* host, size_t bytes);
 
 #ifdef __cplusplus
 }

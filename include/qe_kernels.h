@@ -212,6 +212,12 @@ int qe_launch_attention_gqa_prefill(const uint16_t* q, const uint16_t* layer_k_c
  * rocprofv3 FETCH_SIZE.  No counterpart in the reference. */
 int qe_stream_read(const void* data, size_t bytes, uint32_t* sink, hipStream_t stream);
 
+/* Process-wide tuning switches (no counterpart in the reference):
+ *   "gemm_split_k" 0/1 (default 1) - split K across blocks for prefill GEMMs
+ *   whose tile grid leaves CUs idle.  Returns QE_ERR_INVALID_ARGUMENT for an
+ *   unknown key. */
+int qe_set_tuning(const char* key, int value);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,6 +12,7 @@
 // sequence is available with fused_decode = 0.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -323,7 +324,10 @@ extern "C" int qe_engine_create(const qe_engine_config* cfg, uint64_t seed, qe_e
     bytes += 2 * align256(static_cast<size_t>(T) * H * 2) + align256(static_cast<size_t>(T) * qd * 2) +
              2 * align256(static_cast<size_t>(T) * kvd * 2) + align256(static_cast<size_t>(T) * qd * 2) +
              align256(static_cast<size_t>(T) * I * 2) + align256(static_cast<size_t>(c.vocab_size) * 2);
-    bytes += align256(I) + align256(I / 128 * 4) + align256(I / 8 * 4);
+    // Q8_1 scratch holds the longest quantized activation: the down input (I),
+    // the normalized hidden state (H) or the attention output (q_dim)
+    const int QN = std::max(I, std::max(H, qd));
+    bytes += align256(QN) + align256(QN / 128 * 4) + align256(QN / 8 * 4);
     bytes += 2 * align256(static_cast<size_t>(c.num_q_heads) * 16 * 128 * 4) + 2 * align256(256 * 4) +
              align256(static_cast<size_t>(c.max_seq_len) * 4) + 256 + 256 + 4096;
     QE_HIP(hipStreamCreate(&e->stream));
@@ -361,9 +365,9 @@ extern "C" int qe_engine_create(const qe_engine_config* cfg, uint64_t seed, qe_e
     e->attn = e->take<uint16_t>(static_cast<size_t>(T) * qd * 2);
     e->mlp = e->take<uint16_t>(static_cast<size_t>(T) * I * 2);
     e->logits = e->take<uint16_t>(static_cast<size_t>(c.vocab_size) * 2);
-    e->q8 = e->take<int8_t>(I);
-    e->q8_scale = e->take<float>(I / 128 * 4);
-    e->q8_sum8 = e->take<int32_t>(I / 8 * 4);
+    e->q8 = e->take<int8_t>(QN);
+    e->q8_scale = e->take<float>(QN / 128 * 4);
+    e->q8_sum8 = e->take<int32_t>(QN / 8 * 4);
     e->part_o = e->take<float>(static_cast<size_t>(c.num_q_heads) * 16 * 128 * 4);
     e->part_lse = e->take<float>(static_cast<size_t>(c.num_q_heads) * 16 * 2 * 4);
     e->sample_val = e->take<float>(256 * 4);
@@ -496,3 +500,44 @@ extern "C" int qe_engine_seq_pos(const qe_engine* e) { return e ? e->seq_pos : -
 extern "C" const uint16_t* qe_engine_logits(const qe_engine* e) { return e ? e->logits : nullptr; }
 
 extern "C" const uint16_t* qe_engine_hidden(const qe_engine* e) { return e ? e->act0 : nullptr; }
+
+extern "C" int qe_engine_read_logits(qe_engine* e, uint16_t* host, int n) {
+    QE_REQUIRE(e && host && n >= 0 && n <= e->cfg.vocab_size, "engine_read_logits: bad arguments");
+    QE_HIP(hipStreamSynchronize(e->stream));
+    QE_HIP(hipMemcpy(host, e->logits, static_cast<size_t>(n) * 2, hipMemcpyDeviceToHost));
+    return QE_OK;
+}
+
+extern "C" int qe_engine_read_hidden(qe_engine* e, uint16_t* host, int n) {
+    QE_REQUIRE(e && host && n >= 0 && n <= e->cfg.hidden_size * e->cfg.prefill_chunk, "engine_read_hidden: bad arguments");
+    QE_HIP(hipStreamSynchronize(e->stream));
+    QE_HIP(hipMemcpy(host, e->act0, static_cast<size_t>(n) * 2, hipMemcpyDeviceToHost));
+    return QE_OK;
+}
+
+extern "C" int qe_engine_read_buffer(qe_engine* e, const char* name, void* host, size_t bytes) {
+    QE_REQUIRE(e && name && host, "engine_read_buffer: bad arguments");
+    const qe_engine_config& c = e->cfg;
+    const int qn = std::max(c.intermediate_size, std::max(c.hidden_size, c.num_q_heads * c.head_dim));
+    struct Item { const char* n; const void* p; size_t size; };
+    const Item items[] = {
+        {"logits", e->logits, static_cast<size_t>(c.vocab_size) * 2},
+        {"hidden", e->act0, static_cast<size_t>(c.prefill_chunk) * c.hidden_size * 2},
+        {"q8", e->q8, static_cast<size_t>(qn)},
+        {"q8_scale", e->q8_scale, static_cast<size_t>(qn / 128) * 4},
+        {"q8_sum8", e->q8_sum8, static_cast<size_t>(qn / 8) * 4},
+        {"embed_w", e->embed.w, static_cast<size_t>(c.vocab_size) * c.hidden_size / 2},
+        {"embed_s", e->embed.s, static_cast<size_t>(c.vocab_size) * (c.hidden_size / 128) * 2},
+        {"final_norm", e->final_norm, static_cast<size_t>(c.hidden_size) * 2},
+        {"control", e->ctl, sizeof(qe_device_control_block)},
+    };
+    for (const Item& it : items) {
+        if (std::strcmp(it.n, name) == 0) {
+            QE_REQUIRE(bytes <= it.size, "engine_read_buffer: %zu bytes requested, '%s' holds %zu", bytes, name, it.size);
+            QE_HIP(hipStreamSynchronize(e->stream));
+            QE_HIP(hipMemcpy(host, it.p, bytes, hipMemcpyDeviceToHost));
+            return QE_OK;
+        }
+    }
+    return fail(QE_ERR_INVALID_ARGUMENT, "engine_read_buffer: unknown buffer '%s'", name);
+}

@@ -9,15 +9,20 @@
 // MI355X design:
 //   * 256-thread blocks (4 wave64s in a 2x2 grid), block tile BM x BN with
 //     BM, BN in {64, 128}; each wave owns (BM/2) x (BN/2) as 32x32 tiles of
-//     v_mfma_f32_32x32x16_f16 (fp32 accumulators in VGPR/AGPR).
-//   * K advances 32 at a time.  Per step, one 16-byte load brings the 32
-//     packed int4 of one weight row (exactly one uint4), which a thread
-//     dequantizes to 32 fp16 and stores to LDS; the A tile streams through
-//     16-byte loads.  LDS is double-buffered (one barrier per K step) and
-//     the next step's global loads are issued before the current MFMAs.
-//   * LDS rows are padded to 40 halves (80 B) so the 16-byte fragment reads
-//     of 32 consecutive rows spread over the banks.
-//   * Tile shape is chosen per launch so the grid covers the 256 CUs.
+//     v_mfma_f32_32x32x16_f16 (fp32 accumulators).
+//   * The B operand of a lane (8 consecutive k of one weight column) is one
+//     packed int4 word: each lane loads its 16-byte run of 32 k straight from
+//     global memory and dequantizes it in registers ((q-8) via the 0x6400
+//     bias, one fp16 RNE multiply by the group scale) - no LDS round trip and
+//     no barrier for the weights.  A (fp16 activations) is staged through a
+//     double-buffered LDS tile.  K advances 64 per step; A and B loads run in
+//     a 4-stage register ring, so three steps of loads are in flight.
+//   * Tile shape is chosen per launch so the grid covers the 256 CUs; when
+//     64x64 tiles still leave CUs idle (small M, e.g. K = 8960 at M = 128)
+//     K is split into slices whose fp32 partials a second kernel reduces in
+//     slice order.
+#include <algorithm>
+
 #include "qe_common.hpp"
 
 namespace qe {
@@ -29,8 +34,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kPlain = 0;
 constexpr int kQKV = 1;
 constexpr int kSwiglu = 2;
-constexpr int BK = 32;
-constexpr int LDS_STRIDE = 40;  // halves per LDS row (32 + 8 pad)
+constexpr int BK = 64;
+constexpr int A_STRIDE = 72;  // halves per LDS row of the A tile (64 + 8 pad)
 
 struct GemmParams {
     const uint32_t* qw[3];
@@ -45,116 +50,21 @@ struct GemmParams {
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
+// Split-K scratch: fp32 partial tiles of the K slices, reduced by a second
+// kernel on the same stream (deterministic order, no atomics or fences).  A
+// file-scope device array, so launches stay allocation-free and
+// graph-capture safe.  Split-K launches issued concurrently on different
+// streams of one device would share it; the engine issues its GEMMs on one
+// stream.
+constexpr size_t kWsFloats = size_t(8) << 20;  // 32 MiB
+__device__ float g_splitk_ws[kWsFloats];
+
 template <int BM, int BN, int MODE>
-__global__ __launch_bounds__(256) void gemm_w4a16_mfma_kernel(GemmParams p) {
-    constexpr int WM = BM / 2;  // rows per wave
-    constexpr int WN = BN / 2;  // cols per wave
-    constexpr int MI = WM / 32;
-    constexpr int NI = WN / 32;
-    constexpr int A_U4 = BM * BK / 8 / 256;  // uint4 (8 halves) per thread for the A tile: 1 or 2
-    static_assert(A_U4 >= 1, "tile too small");
-
-    __shared__ __align__(16) _Float16 sA[2][BM * LDS_STRIDE];
-    __shared__ __align__(16) _Float16 sB[2][BN * LDS_STRIDE];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM;
-    const int n0 = blockIdx.x * BN;
-    const int K = p.K;
-    const int G = K >> 7;
-    const int KT = K / BK;
-
-    // ---- per-thread load assignments -----------------------------------
-    // A: thread covers A_U4 consecutive uint4 of one row: row = tid / (4/A_U4)
-    const int a_per_row = 4 / A_U4;            // threads per A row (BK/8 = 4 uint4 per row)
-    const int a_row = tid / a_per_row;
-    const int a_col = (tid % a_per_row) * A_U4 * 8;  // halves
-    const int a_grow = m0 + a_row;
-    const bool a_ok = a_row < BM && a_grow < p.M;
-    const uint16_t* a_src = p.A + static_cast<size_t>(a_ok ? a_grow : 0) * K + a_col;
-    // B: thread < BN owns weight row n0 + tid
-    const bool b_thread = tid < BN;
-    const int b_vcol = n0 + tid;
-    bool b_ok = b_thread && b_vcol < p.N;
-    const uint32_t* b_src = nullptr;
-    const uint16_t* b_sc = nullptr;
-    if (b_ok) {
-        int m = 0, local = b_vcol;
-        if constexpr (MODE == kQKV) {
-            m = (b_vcol >= p.col_begin[1]) + (b_vcol >= p.col_begin[2]);
-            local = b_vcol - p.col_begin[m];
-        }
-        b_src = p.qw[m] + static_cast<size_t>(local) * (K >> 3);
-        b_sc = p.sc[m] + static_cast<size_t>(local) * G;
-    }
-
-    uint4 a_reg[A_U4];
-    uint4 b_reg = make_uint4(0, 0, 0, 0);
-    uint16_t b_s = 0;
-
-    auto load_global = [&](int kt) {
-        const int k0 = kt * BK;
-#pragma unroll
-        for (int i = 0; i < A_U4; ++i)
-            a_reg[i] = a_ok ? *reinterpret_cast<const uint4*>(a_src + k0 + i * 8) : make_uint4(0, 0, 0, 0);
-        if (b_ok) {
-            b_reg = *reinterpret_cast<const uint4*>(b_src + (k0 >> 3));
-            b_s = b_sc[k0 >> 7];
-        }
-    };
-    auto store_lds = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < A_U4; ++i)
-            *reinterpret_cast<uint4*>(&sA[buf][a_row * LDS_STRIDE + a_col + i * 8]) = a_reg[i];
-        if (b_thread) {
-            const _Float16 s = __builtin_bit_cast(_Float16, b_s);
-            const uint32_t w[4] = {b_reg.x, b_reg.y, b_reg.z, b_reg.w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                qwen::qe_half8_t h = b_ok ? qwen::unpack_w4_to_half8(w[j], s) : qwen::qe_half8_t{};
-                *reinterpret_cast<qwen::qe_half8_t*>(&sB[buf][tid * LDS_STRIDE + j * 8]) = h;
-            }
-        }
-    };
-
-    f32x16 acc[MI][NI];
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
-
-    load_global(0);
-    store_lds(0);
-    __syncthreads();
-
-    const int fr = lane & 31;        // fragment row (A) / column (B)
-    const int fk = (lane >> 5) * 8;  // k offset of the lane's 8 halves
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < KT) load_global(kt + 1);
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 16) {
-            f16x8 af[MI], bf[NI];
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-                af[i] = *reinterpret_cast<const f16x8*>(&sA[buf][(wm * WM + i * 32 + fr) * LDS_STRIDE + kk + fk]);
-#pragma unroll
-            for (int j = 0; j < NI; ++j)
-                bf[j] = *reinterpret_cast<const f16x8*>(&sB[buf][(wn * WN + j * 32 + fr) * LDS_STRIDE + kk + fk]);
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int j = 0; j < NI; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < KT) store_lds(buf ^ 1);
-        __syncthreads();
-    }
-
-    // ---- epilogue: D[i][j], j = lane%32, i = 8*(v/4) + 4*(lane/32) + v%4 ----
+__device__ __forceinline__ void epilogue(const GemmParams& p, const f32x16 (&acc)[BM / 64][BN / 64], int m0, int n0,
+                                         int wm, int wn, int lane) {
+    constexpr int WM = BM / 2, WN = BN / 2, MI = WM / 32, NI = WN / 32;
+    const int fr = lane & 31;
+    // D[i][j] of a 32x32 MFMA tile: j = lane%32, i = 8*(v/4) + 4*(lane/32) + v%4
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
 #pragma unroll
@@ -187,22 +97,203 @@ __global__ __launch_bounds__(256) void gemm_w4a16_mfma_kernel(GemmParams p) {
     }
 }
 
+// Block tile BM x BN, 4 waves in a 2x2 grid, wave tile (BM/2) x (BN/2) of
+// 32x32 MFMA tiles.  K advances BK = 64 per step.  grid (N tiles, M tiles,
+// K slices); with more than one slice the fp32 partials go to the scratch.
+//
+// Operand layout.  v_mfma_f32_32x32x16_f16 takes, per lane l, 8 consecutive
+// k of A row (l % 32) and of B column (l % 32), the lane half h = l / 32
+// holding the second 8.  The k order inside the instruction is free as long
+// as A and B agree, so within a 64-wide step lane half h takes k in
+// [32h, 32h + 32) and sub-step s the 8 values at 8s: for B that is word s of
+// one 16-byte load of packed int4 - the lane's B operand comes straight from
+// global memory and is dequantized in registers (no LDS for B).  A is staged
+// through LDS (rows padded to 72 halves: conflict-free 16-byte reads).
+template <int BM, int BN, int MODE>
+__global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int MI = WM / 32, NI = WN / 32;
+    constexpr int A_U4 = BM * BK / 8 / 256;  // 16-byte A chunks per thread per step (4 or 2)
+    // A rows are loaded 8 threads per 128-byte row, 32 rows per pass
+    constexpr int D = (BM == 128 && BN == 128) ? 3 : 4;  // stages of the register ring
+    static_assert(A_U4 * 32 == BM, "A tile passes");
+
+    __shared__ __align__(16) _Float16 sA[2][BM * A_STRIDE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM;
+    const int n0 = blockIdx.x * BN;
+    const int K = p.K;
+    const int G = K >> 7;
+    const int KT_all = K / BK;
+    const int slices = gridDim.z;
+    const int kt_begin = static_cast<int>((static_cast<long long>(blockIdx.z) * KT_all) / slices);
+    const int kt_end = static_cast<int>((static_cast<long long>(blockIdx.z + 1) * KT_all) / slices);
+    const int KT = kt_end - kt_begin;
+    const int fr = lane & 31;
+    const int h = lane >> 5;
+
+    // A: rows past M read row M-1 (valid) and are never stored
+    const int a_row = tid >> 3;
+    const int a_col = (tid & 7) * 8;  // halves
+    const uint16_t* a_src[A_U4];
+#pragma unroll
+    for (int i = 0; i < A_U4; ++i)
+        a_src[i] = p.A + static_cast<size_t>(min(m0 + a_row + 32 * i, p.M - 1)) * K + a_col;
+    // B: lane's column for fragment j; columns past N read column N-1
+    const u32x4* b_src[NI];
+    const uint16_t* b_sc[NI];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        const int col = min(n0 + wn * WN + j * 32 + fr, p.N - 1);
+        int m = 0, local = col;
+        if constexpr (MODE == kQKV) {
+            m = (col >= p.col_begin[1]) + (col >= p.col_begin[2]);
+            local = col - p.col_begin[m];
+        }
+        b_src[j] = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(local) * (K >> 3)) + h;
+        b_sc[j] = p.sc[m] + static_cast<size_t>(local) * G;
+    }
+
+    struct Stage {
+        u32x4 a[A_U4];
+        u32x4 b[NI];
+        uint16_t s[NI];
+    };
+    Stage st[D];
+    auto load_global = [&](int kt, Stage& S) __attribute__((always_inline)) {
+        const int k0 = (kt_begin + kt) * BK;
+#pragma unroll
+        for (int i = 0; i < A_U4; ++i) S.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            S.b[j] = __builtin_nontemporal_load(b_src[j] + (k0 >> 5));  // 16 B = 32 k of lane half h
+            S.s[j] = b_sc[j][k0 >> 7];
+        }
+    };
+    auto store_a = [&](int buf, const Stage& S) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < A_U4; ++i)
+            *reinterpret_cast<u32x4*>(&sA[buf][(a_row + 32 * i) * A_STRIDE + a_col]) = S.a[i];
+    };
+
+    f32x16 acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
+
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_global(min(d, KT - 1), st[d]);
+    store_a(0, st[0]);
+    __syncthreads();
+
+    auto step = [&](int kt, int d) __attribute__((always_inline)) {
+        const int buf = kt & 1;
+        const Stage& S = st[d];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            f16x8 af[MI], bf[NI];
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+                af[i] = *reinterpret_cast<const f16x8*>(&sA[buf][(wm * WM + i * 32 + fr) * A_STRIDE + h * 32 + s * 8]);
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+                bf[j] = __builtin_bit_cast(f16x8, qwen::unpack_w4_to_half8(S.b[j][s], __builtin_bit_cast(_Float16, S.s[j])));
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        load_global(min(kt + D, KT - 1), st[d]);  // step kt is consumed: refill with step kt + D
+        store_a(buf ^ 1, st[(d + 1) % D]);          // A of step kt + 1, loaded D - 1 steps ago
+        __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + D <= KT; kt += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) step(kt + d, d);
+    }
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d)
+        if (kt + d < KT) step(kt + d, d);  // tail: fewer than D steps
+
+    if (slices == 1) {
+        epilogue<BM, BN, MODE>(p, acc, m0, n0, wm, wn, lane);
+        return;
+    }
+    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const int n_tiles = gridDim.x * gridDim.y;
+    float* mine = g_splitk_ws + (static_cast<size_t>(blockIdx.z) * n_tiles + tile) * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) mine[((i * NI + j) * 16 + v) * 256 + tid] = acc[i][j][v];
+}
+
+// Sums the K-slice partials of each tile in slice order and applies the
+// epilogue.  grid (N tiles, M tiles), 256 threads (the MFMA lane layout).
+template <int BM, int BN, int MODE>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, int slices) {
+    constexpr int MI = BM / 64, NI = BN / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const int n_tiles = gridDim.x * gridDim.y;
+    f32x16 acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
+    for (int z = 0; z < slices; ++z) {
+        const float* part = g_splitk_ws + (static_cast<size_t>(z) * n_tiles + tile) * (BM * BN);
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][j][v] += part[((i * NI + j) * 16 + v) * 256 + tid];
+    }
+    epilogue<BM, BN, MODE>(p, acc, blockIdx.y * BM, blockIdx.x * BN, wave >> 1, wave & 1, lane);
+}
+
+template <int BM, int BN, int MODE>
+void launch_tiles(const GemmParams& p, int slices, hipStream_t s) {
+    const dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, slices);
+    gemm_w4a16_mfma_kernel<BM, BN, MODE><<<grid, 256, 0, s>>>(p);
+    if (slices > 1) gemm_splitk_reduce_kernel<BM, BN, MODE><<<dim3(grid.x, grid.y), 256, 0, s>>>(p, slices);
+}
+
 template <int MODE>
 int launch_gemm(const GemmParams& p, hipStream_t stream, const char* what) {
     if (p.M <= 0 || p.N <= 0) return QE_OK;
     const int cus = cu_count();
-    auto blocks = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
-    // largest tile that still gives >= 1 block per CU; else the smallest tile
+    auto tiles = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
+    // largest tile that still gives >= 1 block per CU; else 64x64 tiles and K slices
     int bm = 64, bn = 64;
-    if (blocks(128, 128) >= cus) { bm = 128; bn = 128; }
-    else if (blocks(64, 128) >= cus) { bm = 64; bn = 128; }
-    else if (blocks(128, 64) >= cus) { bm = 128; bn = 64; }
-    const dim3 grid((p.N + bn - 1) / bn, (p.M + bm - 1) / bm);
-    if (grid.y > 65535) return fail(QE_ERR_UNSUPPORTED, "%s: M=%d too large", what, p.M);
-    if (bm == 128 && bn == 128) gemm_w4a16_mfma_kernel<128, 128, MODE><<<grid, 256, 0, stream>>>(p);
-    else if (bm == 64 && bn == 128) gemm_w4a16_mfma_kernel<64, 128, MODE><<<grid, 256, 0, stream>>>(p);
-    else if (bm == 128 && bn == 64) gemm_w4a16_mfma_kernel<128, 64, MODE><<<grid, 256, 0, stream>>>(p);
-    else gemm_w4a16_mfma_kernel<64, 64, MODE><<<grid, 256, 0, stream>>>(p);
+    if (tiles(128, 128) >= cus) { bm = 128; bn = 128; }
+    else if (tiles(64, 128) >= cus) { bm = 64; bn = 128; }
+    else if (tiles(128, 64) >= cus) { bm = 128; bn = 64; }
+    const int nt = tiles(bm, bn);
+    const int KT = p.K / BK;
+    int slices = 1;
+    if (nt < cus && gemm_split_k_enabled()) {
+        slices = (2 * cus + nt - 1) / nt;   // about two blocks per CU
+        slices = std::min(slices, KT / 8);  // >= 8 steps of 64 per slice
+        slices = std::min(slices, 32);
+        slices = std::max(slices, 1);
+        while (slices > 1 && static_cast<size_t>(slices) * nt * bm * bn > kWsFloats) --slices;
+    }
+    if ((p.M + bm - 1) / bm > 65535) return fail(QE_ERR_UNSUPPORTED, "%s: M=%d too large", what, p.M);
+    if (bm == 128 && bn == 128) launch_tiles<128, 128, MODE>(p, slices, stream);
+    else if (bm == 64 && bn == 128) launch_tiles<64, 128, MODE>(p, slices, stream);
+    else if (bm == 128 && bn == 64) launch_tiles<128, 64, MODE>(p, slices, stream);
+    else launch_tiles<64, 64, MODE>(p, slices, stream);
     return check_launch(what);
 }
 

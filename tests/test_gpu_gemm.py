@@ -125,3 +125,26 @@ def test_gemm_rejects_bad_k(qe):
     with pytest.raises(RuntimeError, match="multiple of 128"):
         qe.launch_gemm_prefill_w4a16(empty(10, torch.int32), empty(10, torch.float16), empty(100, torch.float16),
                                      None, empty(4, torch.float16), 1, 4, 100)
+
+
+def test_gemm_split_k_deterministic_across_interleaved_launches(qe, orc):
+    """Small-M shapes reduce K across blocks through the shared scratch: results
+    are bit-identical launch after launch, with other split-K shapes in between."""
+    shapes = [(40, 2048, 1536), (40, 1536, 8960), (40, 1536, 1536), (7, 512, 4096), (128, 1536, 8960)]
+    data = []
+    for (M, N, K) in shapes:
+        qw, sc = orc.synth_w4(M * 3 + N + K, N, K)
+        A = _A(orc, M, K, N)
+        data.append((dev(qw), dev(sc), dev(A), empty((M, N), torch.float16), M, N, K, qw, sc, A))
+    first = []
+    for rep in range(12):
+        for i, (dqw, dsc, dA, out, M, N, K, *_r) in enumerate(data):
+            qe.launch_gemm_prefill_w4a16(dqw, dsc, dA, None, out, M, N, K)
+            got = host(out)
+            if rep == 0:
+                first.append(got.copy())
+            else:
+                assert np.array_equal(got.view(np.uint16), first[i].view(np.uint16)), f"rep {rep} shape {i}"
+    for i, (dqw, dsc, dA, out, M, N, K, qw, sc, A) in enumerate(data):
+        ref, ex, bd = orc.gemm_w4a16(qw, sc, A, M, N, K)
+        assert_fp16_close(first[i], ex, bd, ref, what=f"split-K shape {i}")
