@@ -214,8 +214,11 @@ int qe_stream_read(const void* data, size_t bytes, uint32_t* sink, hipStream_t s
 
 /* Process-wide tuning switches (no counterpart in the reference):
  *   "gemm_split_k" 0/1 (default 1) - split K across blocks for prefill GEMMs
- *   whose tile grid leaves CUs idle.  Returns QE_ERR_INVALID_ARGUMENT for an
- *   unknown key. */
+ *   whose tile grid leaves CUs idle;
+ *   "gemm_tile" 0..4 (default 0 = chosen per shape) - force the prefill GEMM
+ *   block tile: 1 64x64, 2 64x128, 3 128x64, 4 128x128 (rows x columns);
+ *   "gemm_slices" 0..64 (default 0 = chosen per shape) - force the number of
+ *   K slices.  Returns QE_ERR_INVALID_ARGUMENT for an unknown key or value. */
 int qe_set_tuning(const char* key, int value);
 
 #ifdef __cplusplus

@@ -110,11 +110,14 @@ typedef _Float16 qe_half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 qe_half8_t __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ qe_half8_t unpack_w4_to_half8(uint32_t packed, _Float16 scale) {
-    const uint32_t bias1024 = 0x64006400u;
-    uint32_t u01 = (packed & 0x000Fu) | ((packed & 0x0F00u) << 8) | bias1024;
-    uint32_t u23 = ((packed >> 16) & 0x000Fu) | ((packed >> 8) & 0x000F0000u) | bias1024;
-    uint32_t u45 = ((packed >> 4) & 0x000Fu) | ((packed << 4) & 0x000F0000u) | bias1024;
-    uint32_t u67 = ((packed >> 20) & 0x000Fu) | ((packed >> 12) & 0x000F0000u) | bias1024;
+    // bytes (q0|q4<<4, 0x64, q1|q5<<4, 0x64) and (q2|q6<<4, 0x64, q3|q7<<4, 0x64):
+    // masking the high nibble of the even bytes gives 0x6400|q as fp16 pairs
+    const uint32_t x01 = __builtin_amdgcn_perm(0x64646464u, packed, 0x04010400u);
+    const uint32_t x23 = __builtin_amdgcn_perm(0x64646464u, packed, 0x04030402u);
+    const uint32_t u01 = x01 & 0xFF0FFF0Fu;
+    const uint32_t u23 = x23 & 0xFF0FFF0Fu;
+    const uint32_t u45 = ((x01 >> 4) & 0x000F000Fu) | 0x64006400u;
+    const uint32_t u67 = ((x23 >> 4) & 0x000F000Fu) | 0x64006400u;
     const qe_half2_t b = {(_Float16)1032.0f, (_Float16)1032.0f};
     const qe_half2_t s = {scale, scale};
     qe_half2_t h01 = (__builtin_bit_cast(qe_half2_t, u01) - b) * s;

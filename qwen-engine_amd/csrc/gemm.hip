@@ -7,20 +7,21 @@
 // outputs (:392-489); gate/up SwiGLU over interleaved columns (:559-609).
 //
 // MI355X design:
-//   * 256-thread blocks (4 wave64s in a 2x2 grid), block tile BM x BN with
-//     BM, BN in {64, 128}; each wave owns (BM/2) x (BN/2) as 32x32 tiles of
-//     v_mfma_f32_32x32x16_f16 (fp32 accumulators).
+//   * 256-thread blocks (4 wave64s), block tiles 64x64 and 128x64 with the
+//     waves in a 2x2 grid, 64x128 and 128x128 with the waves side by side
+//     (1x4: each wave owns all BM rows and 32 columns, so no two waves
+//     dequantize the same weights); 32x32 tiles of
+//     v_mfma_f32_32x32x16_f16 with fp32 accumulators.
 //   * The B operand of a lane (8 consecutive k of one weight column) is one
 //     packed int4 word: each lane loads its 16-byte run of 32 k straight from
 //     global memory and dequantizes it in registers ((q-8) via the 0x6400
 //     bias, one fp16 RNE multiply by the group scale) - no LDS round trip and
 //     no barrier for the weights.  A (fp16 activations) is staged through a
-//     double-buffered LDS tile.  K advances 64 per step; A and B loads run in
-//     a 4-stage register ring, so three steps of loads are in flight.
-//   * Tile shape is chosen per launch so the grid covers the 256 CUs; when
-//     64x64 tiles still leave CUs idle (small M, e.g. K = 8960 at M = 128)
-//     K is split into slices whose fp32 partials a second kernel reduces in
-//     slice order.
+//     double-buffered LDS tile.  K advances 64 per step; A loads run in a
+//     4-stage register ring, weights a whole 256-k quad ahead.
+//   * Tile shape and K slices are chosen per launch from a fitted time model
+//     (blocks per CU, steps per block, split-K overhead); split-K partials
+//     are reduced by a second kernel in slice order.
 #include <algorithm>
 
 #include "qe_common.hpp"
@@ -59,10 +60,10 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 constexpr size_t kWsFloats = size_t(8) << 20;  // 32 MiB
 __device__ float g_splitk_ws[kWsFloats];
 
-template <int BM, int BN, int MODE>
-__device__ __forceinline__ void epilogue(const GemmParams& p, const f32x16 (&acc)[BM / 64][BN / 64], int m0, int n0,
-                                         int wm, int wn, int lane) {
-    constexpr int WM = BM / 2, WN = BN / 2, MI = WM / 32, NI = WN / 32;
+template <int BM, int BN, int WGM, int MODE>
+__device__ __forceinline__ void epilogue(const GemmParams& p, const f32x16 (&acc)[BM / WGM / 32][BN / (4 / WGM) / 32],
+                                         int m0, int n0, int wm, int wn, int lane) {
+    constexpr int WM = BM / WGM, WN = BN / (4 / WGM), MI = WM / 32, NI = WN / 32;
     const int fr = lane & 31;
     // D[i][j] of a 32x32 MFMA tile: j = lane%32, i = 8*(v/4) + 4*(lane/32) + v%4
 #pragma unroll
@@ -97,52 +98,66 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const f32x16 (&acc
     }
 }
 
-// Block tile BM x BN, 4 waves in a 2x2 grid, wave tile (BM/2) x (BN/2) of
-// 32x32 MFMA tiles.  K advances BK = 64 per step.  grid (N tiles, M tiles,
-// K slices); with more than one slice the fp32 partials go to the scratch.
+// Block tile BM x BN, 4 waves in a WGM x (4/WGM) grid, wave tile WM x WN of
+// 32x32 MFMA tiles.  K advances 64 per step.  grid (N tiles, M tiles, K
+// slices); with more than one slice the fp32 partials go to the scratch.
 //
 // Operand layout.  v_mfma_f32_32x32x16_f16 takes, per lane l, 8 consecutive
 // k of A row (l % 32) and of B column (l % 32), the lane half h = l / 32
 // holding the second 8.  The k order inside the instruction is free as long
-// as A and B agree, so within a 64-wide step lane half h takes k in
-// [32h, 32h + 32) and sub-step s the 8 values at 8s: for B that is word s of
-// one 16-byte load of packed int4 - the lane's B operand comes straight from
-// global memory and is dequantized in registers (no LDS for B).  A is staged
-// through LDS (rows padded to 72 halves: conflict-free 16-byte reads).
-template <int BM, int BN, int MODE>
+// as A and B agree, and that freedom is used to feed B straight from global
+// memory: one packed int4 word is exactly the 8 k of one lane's operand, so
+// each lane dequantizes its own words in registers and the weights never go
+// through LDS.  A (fp16 activations) is staged through a double-buffered
+// LDS tile (rows padded to 72 halves: conflict-free 16-byte reads).
+//
+// QUAD (K % 256 == 0): weights are read 256 k at a time, one 128-byte line
+// per column - lane half h loads the 64 bytes of k in [128h, 128h + 128) as
+// four 16-byte loads, with its single group scale - and the four 64-k steps
+// of the quad take k = 128h + 32t + 8s in step t, sub-step s.  A step then
+// spans two 32-k pieces of A, 128 k apart.  Without QUAD each step loads
+// 16 bytes per lane (k = 32h + 8s) and one scale.
+template <int BM, int BN, int WGM, int MODE, bool QUAD>
 __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
-    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int WGN = 4 / WGM;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int MI = WM / 32, NI = WN / 32;
-    constexpr int A_U4 = BM * BK / 8 / 256;  // 16-byte A chunks per thread per step (4 or 2)
-    // A rows are loaded 8 threads per 128-byte row, 32 rows per pass
-    constexpr int D = (BM == 128 && BN == 128) ? 3 : 4;  // stages of the register ring
-    static_assert(A_U4 * 32 == BM, "A tile passes");
+    constexpr int A_U4 = BM / 32;  // 16-byte A chunks per thread per step: 8 threads per row, 32 rows per pass
+    constexpr int D = (QUAD || BM == 64) ? 4 : 3;  // stages of the A register ring
+    static_assert(MI >= 1 && NI >= 1, "wave tile");
 
     __shared__ __align__(16) _Float16 sA[2][BM * A_STRIDE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WGN, wn = wave % WGN;
     const int m0 = blockIdx.y * BM;
     const int n0 = blockIdx.x * BN;
     const int K = p.K;
     const int G = K >> 7;
-    const int KT_all = K / BK;
     const int slices = gridDim.z;
-    const int kt_begin = static_cast<int>((static_cast<long long>(blockIdx.z) * KT_all) / slices);
-    const int kt_end = static_cast<int>((static_cast<long long>(blockIdx.z + 1) * KT_all) / slices);
+    constexpr int UNIT = QUAD ? 4 : 1;  // steps per slicing unit
+    const int U_all = K / (BK * UNIT);
+    const int kt_begin = UNIT * static_cast<int>((static_cast<long long>(blockIdx.z) * U_all) / slices);
+    const int kt_end = UNIT * static_cast<int>((static_cast<long long>(blockIdx.z + 1) * U_all) / slices);
     const int KT = kt_end - kt_begin;
     const int fr = lane & 31;
     const int h = lane >> 5;
 
     // A: rows past M read row M-1 (valid) and are never stored
     const int a_row = tid >> 3;
-    const int a_col = (tid & 7) * 8;  // halves
+    const int c = tid & 7;
+    const int a_col = c * 8;  // halves within the LDS row
+    const int a_k = QUAD ? 128 * (c >> 2) + 8 * (c & 3) : 8 * c;
     const uint16_t* a_src[A_U4];
 #pragma unroll
     for (int i = 0; i < A_U4; ++i)
-        a_src[i] = p.A + static_cast<size_t>(min(m0 + a_row + 32 * i, p.M - 1)) * K + a_col;
+        a_src[i] = p.A + static_cast<size_t>(min(m0 + a_row + 32 * i, p.M - 1)) * K + a_k;
+    auto a_koff = [&](int kt) __attribute__((always_inline)) {
+        const int g = kt_begin + kt;
+        return QUAD ? 256 * (g >> 2) + 32 * (g & 3) : 64 * g;
+    };
     // B: lane's column for fragment j; columns past N read column N-1
     const u32x4* b_src[NI];
     const uint16_t* b_sc[NI];
@@ -154,30 +169,33 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
             m = (col >= p.col_begin[1]) + (col >= p.col_begin[2]);
             local = col - p.col_begin[m];
         }
-        b_src[j] = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(local) * (K >> 3)) + h;
-        b_sc[j] = p.sc[m] + static_cast<size_t>(local) * G;
+        b_src[j] = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(local) * (K >> 3)) + (QUAD ? 4 : 1) * h;
+        b_sc[j] = p.sc[m] + static_cast<size_t>(local) * G + (QUAD ? h : 0);
     }
 
-    struct Stage {
-        u32x4 a[A_U4];
-        u32x4 b[NI];
-        uint16_t s[NI];
-    };
-    Stage st[D];
-    auto load_global = [&](int kt, Stage& S) __attribute__((always_inline)) {
-        const int k0 = (kt_begin + kt) * BK;
+    u32x4 ra[D][A_U4];
+    u32x4 rb[QUAD ? 2 : D][NI][QUAD ? 4 : 1];
+    uint16_t rs[QUAD ? 2 : D][NI];
+    auto load_a = [&](int kt, int d) __attribute__((always_inline)) {
+        const int k0 = a_koff(kt);
 #pragma unroll
-        for (int i = 0; i < A_U4; ++i) S.a[i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
+        for (int i = 0; i < A_U4; ++i) ra[d][i] = *reinterpret_cast<const u32x4*>(a_src[i] + k0);
+    };
+    // QUAD: quad qd (relative to the slice) into buffer e; else step qd into ring slot e
+    auto load_b = [&](int qd, int e) __attribute__((always_inline)) {
+        const int g = (kt_begin / UNIT) + qd;
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
-            S.b[j] = __builtin_nontemporal_load(b_src[j] + (k0 >> 5));  // 16 B = 32 k of lane half h
-            S.s[j] = b_sc[j][k0 >> 7];
+#pragma unroll
+            for (int i = 0; i < (QUAD ? 4 : 1); ++i)
+                rb[e][j][i] = __builtin_nontemporal_load(b_src[j] + (QUAD ? 8 * g + i : 2 * g));
+            rs[e][j] = b_sc[j][QUAD ? 2 * g : (g >> 1)];
         }
     };
-    auto store_a = [&](int buf, const Stage& S) __attribute__((always_inline)) {
+    auto store_a = [&](int buf, int d) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < A_U4; ++i)
-            *reinterpret_cast<u32x4*>(&sA[buf][(a_row + 32 * i) * A_STRIDE + a_col]) = S.a[i];
+            *reinterpret_cast<u32x4*>(&sA[buf][(a_row + 32 * i) * A_STRIDE + a_col]) = ra[d][i];
     };
 
     f32x16 acc[MI][NI];
@@ -187,13 +205,21 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
         for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
 
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_global(min(d, KT - 1), st[d]);
-    store_a(0, st[0]);
+    for (int d = 0; d < D; ++d) load_a(min(d, KT - 1), d);
+    if constexpr (QUAD) {
+        load_b(0, 0);
+    } else {
+#pragma unroll
+        for (int d = 0; d < D; ++d) load_b(min(d, KT - 1), d);
+    }
+    store_a(0, 0);
     __syncthreads();
 
-    auto step = [&](int kt, int d) __attribute__((always_inline)) {
+    // step kt: A ring slot d = kt % D; QUAD: weight buffer e = (kt / 4) % 2,
+    // t = kt % 4; else weight ring slot e = d
+    auto step = [&](int kt, int d, int e, int t) __attribute__((always_inline)) {
         const int buf = kt & 1;
-        const Stage& S = st[d];
+        if (QUAD && t == 0) load_b(min(kt / 4 + 1, KT / 4 - 1), e ^ 1);  // next quad
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             f16x8 af[MI], bf[NI];
@@ -201,29 +227,52 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
             for (int i = 0; i < MI; ++i)
                 af[i] = *reinterpret_cast<const f16x8*>(&sA[buf][(wm * WM + i * 32 + fr) * A_STRIDE + h * 32 + s * 8]);
 #pragma unroll
-            for (int j = 0; j < NI; ++j)
-                bf[j] = __builtin_bit_cast(f16x8, qwen::unpack_w4_to_half8(S.b[j][s], __builtin_bit_cast(_Float16, S.s[j])));
+            for (int j = 0; j < NI; ++j) {
+                const uint32_t w = QUAD ? rb[e][j][t][s] : rb[e][j][0][s];
+                bf[j] = __builtin_bit_cast(f16x8, qwen::unpack_w4_to_half8(w, __builtin_bit_cast(_Float16, rs[e][j])));
+            }
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < NI; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        load_global(min(kt + D, KT - 1), st[d]);  // step kt is consumed: refill with step kt + D
-        store_a(buf ^ 1, st[(d + 1) % D]);          // A of step kt + 1, loaded D - 1 steps ago
+        load_a(min(kt + D, KT - 1), d);      // step kt is consumed: refill with step kt + D
+        if (!QUAD) load_b(min(kt + D, KT - 1), d);
+        store_a(buf ^ 1, (d + 1) % D);        // A of step kt + 1, loaded D - 1 steps ago
+        // scheduling hint: each MFMA followed by one LDS read and three VALU
+        // ops (the dequantization), so the matrix core is fed while they issue
+#pragma unroll
+        for (int i = 0; i < MI * NI * 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        }
         __syncthreads();
     };
     int kt = 0;
-    for (; kt + D <= KT; kt += D) {
+    if constexpr (QUAD) {
+        // KT is a multiple of 4; 8 steps per iteration keep every index static
+        for (; kt + 8 <= KT; kt += 8) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) step(kt + d, d);
+            for (int u = 0; u < 8; ++u) step(kt + u, u % D, u / 4, u % 4);
+        }
+        if (kt < KT) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) step(kt + u, u % D, 0, u);
+        }
+    } else {
+        for (; kt + D <= KT; kt += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) step(kt + d, d, d, 0);
+        }
+#pragma unroll
+        for (int d = 0; d < D - 1; ++d)
+            if (kt + d < KT) step(kt + d, d, d, 0);  // tail: fewer than D steps
     }
-#pragma unroll
-    for (int d = 0; d < D - 1; ++d)
-        if (kt + d < KT) step(kt + d, d);  // tail: fewer than D steps
 
     if (slices == 1) {
-        epilogue<BM, BN, MODE>(p, acc, m0, n0, wm, wn, lane);
+        epilogue<BM, BN, WGM, MODE>(p, acc, m0, n0, wm, wn, lane);
         return;
     }
     const int tile = blockIdx.y * gridDim.x + blockIdx.x;
@@ -239,9 +288,10 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
 
 // Sums the K-slice partials of each tile in slice order and applies the
 // epilogue.  grid (N tiles, M tiles), 256 threads (the MFMA lane layout).
-template <int BM, int BN, int MODE>
+template <int BM, int BN, int WGM, int MODE>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, int slices) {
-    constexpr int MI = BM / 64, NI = BN / 64;
+    constexpr int WGN = 4 / WGM;
+    constexpr int MI = BM / WGM / 32, NI = BN / WGN / 32;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile = blockIdx.y * gridDim.x + blockIdx.x;
     const int n_tiles = gridDim.x * gridDim.y;
@@ -259,41 +309,78 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, i
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] += part[((i * NI + j) * 16 + v) * 256 + tid];
     }
-    epilogue<BM, BN, MODE>(p, acc, blockIdx.y * BM, blockIdx.x * BN, wave >> 1, wave & 1, lane);
+    epilogue<BM, BN, WGM, MODE>(p, acc, blockIdx.y * BM, blockIdx.x * BN, wave / WGN, wave % WGN, lane);
 }
 
-template <int BM, int BN, int MODE>
+template <int BM, int BN, int WGM, int MODE>
 void launch_tiles(const GemmParams& p, int slices, hipStream_t s) {
     const dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, slices);
-    gemm_w4a16_mfma_kernel<BM, BN, MODE><<<grid, 256, 0, s>>>(p);
-    if (slices > 1) gemm_splitk_reduce_kernel<BM, BN, MODE><<<dim3(grid.x, grid.y), 256, 0, s>>>(p, slices);
+    if (p.K % 256 == 0)
+        gemm_w4a16_mfma_kernel<BM, BN, WGM, MODE, true><<<grid, 256, 0, s>>>(p);
+    else
+        gemm_w4a16_mfma_kernel<BM, BN, WGM, MODE, false><<<grid, 256, 0, s>>>(p);
+    if (slices > 1) gemm_splitk_reduce_kernel<BM, BN, WGM, MODE><<<dim3(grid.x, grid.y), 256, 0, s>>>(p, slices);
+}
+
+// Launch-time model of one configuration (tile, K slices), in microseconds,
+// fitted to MI355X measurements of this kernel over M in {128..2048} and the
+// Qwen2.5-1.5B projection shapes.  Blocks run at most two per CU; a CU with
+// two co-resident blocks advances each more slowly than a CU with one.
+struct TileCost {
+    int bm, bn, wgm;
+    float step1, step2;    // us per 64-k step: one block on the CU / two
+    float split, split_mb; // split-K: fixed cost, cost per MB of fp32 partials
+    float fixed;
+};
+constexpr TileCost kTiles[4] = {
+    {64, 64, 2, 0.464f, 0.912f, 5.50f, 0.030f, 1.34f},
+    {64, 128, 1, 0.521f, 1.112f, 6.06f, 0.024f, 3.74f},
+    {128, 64, 2, 0.588f, 1.224f, 6.23f, 0.018f, 4.07f},
+    {128, 128, 1, 0.688f, 1.632f, 33.7f, 0.020f, 7.57f},
+};
+
+float predict_us(const TileCost& t, int M, int N, int K, int slices, int cus) {
+    const long long blocks = static_cast<long long>((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * slices;
+    const float steps = static_cast<float>(K / BK) / slices;
+    const long long slots = 2LL * cus;
+    const long long rounds = (blocks + slots - 1) / slots;
+    const long long last = blocks - (rounds - 1) * slots;
+    float us = t.fixed + static_cast<float>(rounds - 1) * steps * t.step2 + steps * (last <= cus ? t.step1 : t.step2);
+    if (slices > 1) us += t.split + t.split_mb * (static_cast<float>(slices) * M * N * 8.0f / 1e6f);
+    return us;
 }
 
 template <int MODE>
 int launch_gemm(const GemmParams& p, hipStream_t stream, const char* what) {
     if (p.M <= 0 || p.N <= 0) return QE_OK;
     const int cus = cu_count();
-    auto tiles = [&](int bm, int bn) { return ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
-    // largest tile that still gives >= 1 block per CU; else 64x64 tiles and K slices
-    int bm = 64, bn = 64;
-    if (tiles(128, 128) >= cus) { bm = 128; bn = 128; }
-    else if (tiles(64, 128) >= cus) { bm = 64; bn = 128; }
-    else if (tiles(128, 64) >= cus) { bm = 128; bn = 64; }
-    const int nt = tiles(bm, bn);
     const int KT = p.K / BK;
-    int slices = 1;
-    if (nt < cus && gemm_split_k_enabled()) {
-        slices = (2 * cus + nt - 1) / nt;   // about two blocks per CU
-        slices = std::min(slices, KT / 8);  // >= 8 steps of 64 per slice
-        slices = std::min(slices, 32);
-        slices = std::max(slices, 1);
-        while (slices > 1 && static_cast<size_t>(slices) * nt * bm * bn > kWsFloats) --slices;
+    const int max_slices = (p.K % 256 == 0) ? KT / 4 : KT;  // QUAD slices whole 256-k quads
+    auto fits = [&](const TileCost& t, int s) {
+        const size_t tiles = static_cast<size_t>((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
+        return s == 1 || (s <= max_slices && KT / s >= 4 && static_cast<size_t>(s) * tiles * t.bm * t.bn <= kWsFloats);
+    };
+    int ti = 0, slices = 1;
+    float best = 1e30f;
+    for (int i = 0; i < 4; ++i) {
+        for (int s : {1, 2, 3, 4, 6}) {
+            if (s > 1 && !gemm_split_k_enabled()) break;
+            if (!fits(kTiles[i], s)) continue;
+            const float us = predict_us(kTiles[i], p.M, p.N, p.K, s, cus);
+            if (us < best) { best = us; ti = i; slices = s; }
+        }
     }
-    if ((p.M + bm - 1) / bm > 65535) return fail(QE_ERR_UNSUPPORTED, "%s: M=%d too large", what, p.M);
-    if (bm == 128 && bn == 128) launch_tiles<128, 128, MODE>(p, slices, stream);
-    else if (bm == 64 && bn == 128) launch_tiles<64, 128, MODE>(p, slices, stream);
-    else if (bm == 128 && bn == 64) launch_tiles<128, 64, MODE>(p, slices, stream);
-    else launch_tiles<64, 64, MODE>(p, slices, stream);
+    if (const int f = gemm_forced_tile()) ti = f - 1;
+    if (const int f = gemm_forced_slices()) slices = f;
+    while (slices > 1 && !fits(kTiles[ti], slices)) --slices;
+    const TileCost& t = kTiles[ti];
+    if ((p.M + t.bm - 1) / t.bm > 65535) return fail(QE_ERR_UNSUPPORTED, "%s: M=%d too large", what, p.M);
+    switch (ti) {
+        case 0: launch_tiles<64, 64, 2, MODE>(p, slices, stream); break;
+        case 1: launch_tiles<64, 128, 1, MODE>(p, slices, stream); break;
+        case 2: launch_tiles<128, 64, 2, MODE>(p, slices, stream); break;
+        default: launch_tiles<128, 128, 1, MODE>(p, slices, stream); break;
+    }
     return check_launch(what);
 }
 

@@ -24,6 +24,8 @@ int cu_count();
 
 // Tuning switches (qe_set_tuning).
 int gemm_split_k_enabled();
+int gemm_forced_tile();    // 0 auto, 1 64x64, 2 64x128 (1x4 waves), 3 128x64, 4 128x128 (1x4 waves)
+int gemm_forced_slices();  // 0 auto, else K slices
 
 inline int fail(int code, const char* fmt, ...) {
     char buf[512];

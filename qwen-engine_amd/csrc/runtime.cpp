@@ -15,9 +15,13 @@ namespace {
 thread_local char g_last_error[1024] = "";
 int g_cu_count[64] = {0};
 int g_gemm_split_k = 1;
+int g_gemm_tile = 0;
+int g_gemm_slices = 0;
 }  // namespace
 
 int gemm_split_k_enabled() { return g_gemm_split_k; }
+int gemm_forced_tile() { return g_gemm_tile; }
+int gemm_forced_slices() { return g_gemm_slices; }
 
 void set_error(const char* fmt, ...) {
     va_list ap;
@@ -49,6 +53,16 @@ extern "C" int qe_set_tuning(const char* key, int value) {
     if (key == nullptr) return qe::fail(QE_ERR_INVALID_ARGUMENT, "set_tuning: key is NULL");
     if (std::strcmp(key, "gemm_split_k") == 0) {
         qe::g_gemm_split_k = value != 0;
+        return QE_OK;
+    }
+    if (std::strcmp(key, "gemm_tile") == 0) {
+        if (value < 0 || value > 4) return qe::fail(QE_ERR_INVALID_ARGUMENT, "set_tuning: gemm_tile %d not in 0..4", value);
+        qe::g_gemm_tile = value;
+        return QE_OK;
+    }
+    if (std::strcmp(key, "gemm_slices") == 0) {
+        if (value < 0 || value > 64) return qe::fail(QE_ERR_INVALID_ARGUMENT, "set_tuning: gemm_slices %d not in 0..64", value);
+        qe::g_gemm_slices = value;
         return QE_OK;
     }
     return qe::fail(QE_ERR_INVALID_ARGUMENT, "set_tuning: unknown key '%s'", key);
