@@ -173,79 +173,101 @@ __device__ __forceinline__ int32_t chunk_dot(const u32x4 w, const int4 xa, const
     return qwen::dp4a_w4_q8_oct(w.w, xb.z, xb.w, d);
 }
 
+// Pointers of physical row `row`.  QKV: `urow` is a row of the same matrix
+// that is uniform across the wave (the launch guarantees that the matrix
+// boundaries fall on whole blocks), so the matrix choice is scalar and
+// selects between kernel arguments instead of indexing them in memory.
 template <int MODE>
-__device__ __forceinline__ void row_ptrs(const GemvParams& p, int row, const u32x4*& w, const uint16_t*& s, int& m,
-                                         int& local) {
+__device__ __forceinline__ void row_ptrs(const GemvParams& p, int row, int urow, const u32x4*& w, const uint16_t*& s,
+                                         int& m, int& local) {
     m = 0;
     local = row;
+    const uint32_t* qw = p.qw[0];
+    const uint16_t* sc = p.sc[0];
     if constexpr (MODE == kQKV) {
-        m = (row >= p.row_begin[1]) + (row >= p.row_begin[2]);
-        local = row - p.row_begin[m];
+        const int u = __builtin_amdgcn_readfirstlane(urow);
+        m = (u >= p.row_begin[1]) + (u >= p.row_begin[2]);
+        local = row - (m == 0 ? 0 : (m == 1 ? p.row_begin[1] : p.row_begin[2]));
+        qw = m == 0 ? p.qw[0] : (m == 1 ? p.qw[1] : p.qw[2]);
+        sc = m == 0 ? p.sc[0] : (m == 1 ? p.sc[1] : p.sc[2]);
+    } else {
+        (void)urow;
     }
-    w = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(local) * (p.K >> 3));
-    s = p.sc[m] + static_cast<size_t>(local) * (p.K >> 7);
+    w = reinterpret_cast<const u32x4*>(qw + static_cast<size_t>(local) * (p.K >> 3));
+    s = sc + static_cast<size_t>(local) * (p.K >> 7);
 }
 
-// Q8_1 activation slice of lane l of a segment, straight from global:
-// chunks c = l + i*LPR, i < NCH, as q8 (xa, xb), the chunk's summed sum8
-// seed and the group scale.  Chunks past K get a zero slice.  All loads are
-// issued before any use.
-template <int LPR, int NCH>
-__device__ __forceinline__ void load_x_slice_q8(const GemvParams& p, int l, int4 (&xa)[NCH], int4 (&xb)[NCH],
-                                                int32_t (&xsum)[NCH], float (&xd)[NCH]) {
+// Q8_1 activation staged by the whole block: thread t copies chunk
+// c = t + BT*j (32 q8 bytes, its four sum8 words summed, its group scale)
+// into LDS.  stage_issue_q8 requests the loads (clamped, so every thread
+// issues the same count); stage_finish_q8 stores them.
+template <int BT, int MQ>
+__device__ __forceinline__ void stage_issue_q8(const GemvParams& p, u32x4 (&qa)[MQ], u32x4 (&qb)[MQ],
+                                               int4 (&s4)[MQ], float (&xd)[MQ]) {
     const int KC = p.K >> 5;
-    int4 s4[NCH];
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-        const int cc = min(l + i * LPR, KC - 1);
-        xa[i] = *reinterpret_cast<const int4*>(p.q8 + cc * 32);
-        xb[i] = *reinterpret_cast<const int4*>(p.q8 + cc * 32 + 16);
-        s4[i] = *reinterpret_cast<const int4*>(p.s8 + cc * 4);
-        xd[i] = p.xs[cc >> 2];
+    for (int j = 0; j < MQ; ++j) {
+        const int c = min(static_cast<int>(threadIdx.x) + BT * j, KC - 1);
+        qa[j] = *reinterpret_cast<const u32x4*>(p.q8 + c * 32);
+        qb[j] = *reinterpret_cast<const u32x4*>(p.q8 + c * 32 + 16);
+        s4[j] = *reinterpret_cast<const int4*>(p.s8 + c * 4);
+        xd[j] = p.xs[c >> 2];
     }
+}
+
+// Threads past the last chunk store to a dummy LDS slot (s_rec[KC]) rather
+// than branching: a branch would let the compiler sink the activation loads
+// below the weight loads and wait for both.
+template <int BT, int MQ>
+__device__ __forceinline__ void stage_finish_q8(const GemvParams& p, const u32x4 (&qa)[MQ], const u32x4 (&qb)[MQ],
+                                                const int4 (&s4)[MQ], const float (&xd)[MQ], int8_t* s_q8,
+                                                int2* s_rec) {
+    const int KC = p.K >> 5;
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-        xsum[i] = s4[i].x + s4[i].y + s4[i].z + s4[i].w;
-        if (l + i * LPR >= KC) {
-            xa[i] = xb[i] = make_int4(0, 0, 0, 0);
-            xsum[i] = 0;
-            xd[i] = 0.0f;
-        }
+    for (int j = 0; j < MQ; ++j) {
+        const int c = static_cast<int>(threadIdx.x) + BT * j;
+        const bool ok = c < KC;
+        int8_t* dq = ok ? s_q8 + c * 32 : reinterpret_cast<int8_t*>(s_rec + KC);
+        *reinterpret_cast<u32x4*>(dq) = qa[j];
+        *reinterpret_cast<u32x4*>(dq + 16) = qb[j];
+        s_rec[ok ? c : KC] = make_int2(s4[j].x + s4[j].y + s4[j].z + s4[j].w, __builtin_bit_cast(int, xd[j]));
     }
 }
 
 // fp16 activation staged by the whole block: thread t quantizes the 8
 // elements 8u..8u+7 for u = t + BT*j (a 128-group is one 16-lane DPP row,
 // the quantizer is quantize_group128_q8_1), RMS-normalizing first for kXRMS.
-// All global loads are issued before any arithmetic.  Output in LDS: q8[K]
-// and per 32-element chunk {summed sum8 of its 4 words, scale}.
+// stage_issue_f16 requests the loads (before the weights, so the
+// activation is not queued behind them); stage_finish_f16 computes.  Output
+// in LDS: q8[K] and per 32-element chunk {summed sum8 of its 4 words, scale}.
 template <int XM, int BT, int MAXP>
-__device__ __forceinline__ void stage_block_f16(const GemvParams& p, int8_t* s_q8, int2* s_rec, float* s_red) {
-    const int K = p.K;
-    const int U = K >> 3;  // 8-element units
+__device__ __forceinline__ void stage_issue_f16(const GemvParams& p, uint4 (&raw)[MAXP], uint4 (&graw)[MAXP]) {
+    const int U = p.K >> 3;  // 8-element units
     const int t = threadIdx.x;
-    uint4 raw[MAXP];
 #pragma unroll
     for (int j = 0; j < MAXP; ++j) {
         const int u = min(t + BT * j, U - 1);
         raw[j] = *reinterpret_cast<const uint4*>(p.x16 + 8 * u);
+        if constexpr (XM == kXRMS) graw[j] = *reinterpret_cast<const uint4*>(p.gamma + 8 * u);
     }
+}
+
+template <int XM, int BT, int MAXP>
+__device__ __forceinline__ void stage_finish_f16(const GemvParams& p, uint4 (&raw)[MAXP], const uint4 (&graw)[MAXP],
+                                                 int8_t* s_q8, int2* s_rec, float* s_red) {
+    const int K = p.K;
+    const int U = K >> 3;  // 8-element units
+    const int t = threadIdx.x;
     if constexpr (XM == kXRMS) {
-        uint4 graw[MAXP];
-#pragma unroll
-        for (int j = 0; j < MAXP; ++j) {
-            const int u = min(t + BT * j, U - 1);
-            graw[j] = *reinterpret_cast<const uint4*>(p.gamma + 8 * u);
-        }
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < MAXP; ++j) {
-            if (t + BT * j < U) {
-                float v[8];
-                unpack8(raw[j], v);
+            float v[8];
+            unpack8(raw[j], v);
+            float sj = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
-            }
+            for (int e = 0; e < 8; ++e) sj += v[e] * v[e];
+            ss += (t + BT * j < U) ? sj : 0.0f;
         }
         const float total = block_sum<BT>(ss, s_red);
         const _Float16 h = static_cast<_Float16>(1.0f / sqrtf(total / static_cast<float>(K) + kRmsEps));
@@ -256,27 +278,35 @@ __device__ __forceinline__ void stage_block_f16(const GemvParams& p, int8_t* s_q
             if (write_norm && t + BT * j < U) *reinterpret_cast<uint4*>(p.norm_out + 8 * (t + BT * j)) = raw[j];
         }
     }
+    // every thread quantizes (units past the end repeat the last unit; a
+    // 16-lane row is a whole group, so such rows never mix with real ones)
+    // and stores to a dummy LDS slot (s_rec[KC]) when out of range
+    const int KC = K >> 5;
 #pragma unroll
     for (int j = 0; j < MAXP; ++j) {
-        if (BT * j < U) {  // 16-lane rows are whole groups: they enter or skip together
+        if (BT * j < U) {  // compile-time for the shapes that use one pass
             const int u = t + BT * j;
-            if (u < U) {
-                float vals[8];
-                unpack8(raw[j], vals);
-                const qwen::Q8Group q = qwen::quantize_group128_q8_1(vals);
-                *reinterpret_cast<int2*>(s_q8 + 8 * u) = make_int2(q.x_lo, q.x_hi);
-                int csum = q.sum8;  // chunk = the 4 words of a DPP quad
-                csum += qwen::dpp_i32<0xB1>(csum);
-                csum += qwen::dpp_i32<0x4E>(csum);
-                if ((u & 3) == 0) s_rec[u >> 2] = make_int2(csum, __builtin_bit_cast(int, q.d));
-            }
+            const bool ok = u < U;
+            float vals[8];
+            unpack8(raw[j], vals);
+            const qwen::Q8Group q = qwen::quantize_group128_q8_1(vals);
+            int8_t* dq = ok ? s_q8 + 8 * u : reinterpret_cast<int8_t*>(s_rec + KC);
+            *reinterpret_cast<int2*>(dq) = make_int2(q.x_lo, q.x_hi);
+            int csum = q.sum8;  // chunk = the 4 words of a DPP quad
+            csum += qwen::dpp_i32<0xB1>(csum);
+            csum += qwen::dpp_i32<0x4E>(csum);
+            s_rec[(ok && (u & 3) == 0) ? (u >> 2) : KC] = make_int2(csum, __builtin_bit_cast(int, q.d));
         }
     }
 }
 
-template <int BT, int LPR, int NCH, int RPS, int MODE, int XM>
+template <int BT, int LPR, int NCH, int RPS, int MODE, int XM, bool LOOP>
 __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
-    static_assert(MODE != kSwiglu || RPS == 2, "SwiGLU segments own a (gate, up) row pair");
+    // SwiGLU: a segment owns a (gate, up) row pair (RPS 2), or, with 16-lane
+    // segments and RPS 1, segments 2s and 2s+1 own the gate and up row and
+    // meet through a 32-lane swizzle
+    constexpr bool PAIR = MODE == kSwiglu && RPS == 1;
+    static_assert(MODE != kSwiglu || RPS == 2 || LPR == 16, "SwiGLU row pairing");
     constexpr int SEGS = BT / LPR;
     const int K = p.K;
     const int KC = K >> 5;
@@ -285,18 +315,34 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
     const int n_sets = (p.n_rows + RPS - 1) / RPS;
     const int set_stride = SEGS * gridDim.x;
 
-    // ---- request the first row set before anything else --------------------
+    // ---- activation loads first (a few KB, needed first), then the first
+    //      row set's weights; the activation math overlaps the weight stream.
+    //      Every load is unconditional (indices clamped), so the wait for the
+    //      activation does not also wait for the weights.
+    constexpr int MAXP = (LPR * NCH * 4 + BT - 1) / BT;  // K <= 32*LPR*NCH: 8-element units per thread
+    constexpr int MQ = (LPR * NCH + BT - 1) / BT;        // 32-element chunks per thread (Q8_1 staging)
+    int4 xa[NCH], xb[NCH];
+    int32_t xsum[NCH];
+    float xd[NCH];
+    uint4 raw[XM == kXQ8 ? 1 : MAXP], graw[XM == kXQ8 ? 1 : MAXP];
+    u32x4 qa[XM == kXQ8 ? MQ : 1], qb[XM == kXQ8 ? MQ : 1];
+    int4 qs4[XM == kXQ8 ? MQ : 1];
+    float qxd[XM == kXQ8 ? MQ : 1];
+    if constexpr (XM == kXQ8) stage_issue_q8<BT, MQ>(p, qa, qb, qs4, qxd);
+    else stage_issue_f16<XM, BT, MAXP>(p, raw, graw);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+
     int set = blockIdx.x * SEGS + seg;
     u32x4 w[RPS][NCH];
-    uint16_t hs[RPS][NCH];
-    auto load_set = [&](int st, u32x4 (&wr)[RPS][NCH], uint16_t (&hr)[RPS][NCH]) {
+    uint32_t hs[RPS][NCH];  // fp16 scale bits, one per VGPR (no packing, so no early wait)
+    auto load_set = [&](int st, u32x4 (&wr)[RPS][NCH], uint32_t (&hr)[RPS][NCH]) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < RPS; ++r) {
             const int row = min(st * RPS + r, p.n_rows - 1);  // clamped: tail rows are loaded, not stored
             const u32x4* wp;
             const uint16_t* sp;
             int m, local;
-            row_ptrs<MODE>(p, row, wp, sp, m, local);
+            row_ptrs<MODE>(p, row, min((st - seg) * RPS, p.n_rows - 1), wp, sp, m, local);
 #pragma unroll
             for (int i = 0; i < NCH; ++i) {
                 const int c = min(l + i * LPR, KC - 1);
@@ -305,21 +351,17 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
             }
         }
     };
-    if (set < n_sets) load_set(set, w, hs);
+    load_set(min(set, n_sets - 1), w, hs);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- activation slice in VGPRs ---------------------------------------------
-    int4 xa[NCH], xb[NCH];
-    int32_t xsum[NCH];
-    float xd[NCH];
-    if constexpr (XM == kXQ8) {
-        load_x_slice_q8<LPR, NCH>(p, l, xa, xb, xsum, xd);
-    } else {
+    // ---- activation slice in VGPRs, through LDS ----------------------------------
+    {
         extern __shared__ __align__(16) uint8_t s_mem[];
         __shared__ float s_red[BT / 64];
         int8_t* s_q8 = reinterpret_cast<int8_t*>(s_mem);
         int2* s_rec = reinterpret_cast<int2*>(s_mem + K);
-        // K <= 32 * LPR * NCH, i.e. at most LPR*NCH*4 8-element units
-        stage_block_f16<XM, BT, (LPR * NCH * 4 + BT - 1) / BT>(p, s_q8, s_rec, s_red);
+        if constexpr (XM == kXQ8) stage_finish_q8<BT, MQ>(p, qa, qb, qs4, qxd, s_q8, s_rec);
+        else stage_finish_f16<XM, BT, MAXP>(p, raw, graw, s_q8, s_rec, s_red);
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < NCH; ++i) {
@@ -338,41 +380,51 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
         }
     }
 
-    // ---- stream row sets -----------------------------------------------------
-    for (; set < n_sets; set += set_stride) {
-        u32x4 wn[RPS][NCH];
-        uint16_t hn[RPS][NCH];
-        const int next = set + set_stride;
-        if (next < n_sets) load_set(next, wn, hn);
+    // ---- row sets: one pass, or a grid-stride loop with the next set prefetched
+    auto finish_set = [&](int st) __attribute__((always_inline)) {
         float acc[RPS];
 #pragma unroll
         for (int r = 0; r < RPS; ++r) {
             float a = 0.0f;
 #pragma unroll
             for (int i = 0; i < NCH; ++i)
-                a += static_cast<float>(chunk_dot(w[r][i], xa[i], xb[i], xsum[i])) * (h2f(hs[r][i]) * xd[i]);
+                a += static_cast<float>(chunk_dot(w[r][i], xa[i], xb[i], xsum[i])) *
+                     (h2f(static_cast<uint16_t>(hs[r][i])) * xd[i]);
             acc[r] = qwen::seg_sum<LPR>(a);
         }
-        if (l == 0) {
-            if constexpr (MODE == kSwiglu) {
-                p.out[0][set] = f2h(silu_mul(acc[0], acc[1]));
+        if constexpr (PAIR) acc[0] = silu_mul(acc[0], qwen::swz_xor16_f32(acc[0]));  // gate (even set) x up
+        if (l == 0 && st < n_sets) {
+            if constexpr (PAIR) {
+                if ((st & 1) == 0) p.out[0][st >> 1] = f2h(acc[0]);
+            } else if constexpr (MODE == kSwiglu) {
+                p.out[0][st] = f2h(silu_mul(acc[0], acc[1]));
             } else {
 #pragma unroll
                 for (int r = 0; r < RPS; ++r) {
-                    const int row = set * RPS + r;
+                    const int row = st * RPS + r;
                     if (row < p.n_rows) {
                         const u32x4* wp;
                         const uint16_t* sp;
                         int m, local;
-                        row_ptrs<MODE>(p, row, wp, sp, m, local);
+                        row_ptrs<MODE>(p, row, (st - seg) * RPS, wp, sp, m, local);
                         float v = acc[r];
                         if (MODE == kPlain && p.residual != nullptr) v += h2f(p.residual[local]);
-                        p.out[m][local] = f2h(v);
+                        uint16_t* o = p.out[0];
+                        if constexpr (MODE == kQKV) o = m == 0 ? p.out[0] : (m == 1 ? p.out[1] : p.out[2]);
+                        o[local] = f2h(v);
                     }
                 }
             }
         }
-        if (next < n_sets) {
+    };
+    if constexpr (!LOOP) {
+        finish_set(set);  // the grid covers every set once
+    } else {
+        for (; set < n_sets; set += set_stride) {
+            u32x4 wn[RPS][NCH];
+            uint32_t hn[RPS][NCH];
+            load_set(min(set + set_stride, n_sets - 1), wn, hn);
+            finish_set(set);
 #pragma unroll
             for (int r = 0; r < RPS; ++r)
 #pragma unroll
@@ -411,7 +463,7 @@ __global__ __launch_bounds__(256) void gemv_w4_generic_kernel(GemvParams p) {
             const int row = (MODE == kSwiglu) ? 2 * o + k : o;
             const u32x4* wv;
             const uint16_t* sp;
-            row_ptrs<MODE>(p, row, wv, sp, m, local);
+            row_ptrs<MODE>(p, row, row, wv, sp, m, local);
             const uint32_t* wr = reinterpret_cast<const uint32_t*>(wv);
             float a = 0.0f;
             // word wd covers elements 8wd..8wd+7: chunk wd/4, group wd/16.  The
@@ -455,11 +507,12 @@ Plan plan_for(int K, int n_rows, int mode, bool f16_input) {
         const int n = (KC + 63) / 64;
         pl.nch = n <= 3 ? 3 : (n <= 5 ? 5 : 8);
     }
-    pl.rps = (mode == kSwiglu || n_rows >= 4096) ? 2 : 1;
+    // one row per segment (SwiGLU with 16-lane segments pairs neighbouring
+    // segments); 64-lane SwiGLU segments own a row pair
+    pl.rps = (mode == kSwiglu && pl.lpr == 64) ? 2 : 1;
+    (void)n_rows;
     (void)f16_input;
-    const int sets = (n_rows + pl.rps - 1) / pl.rps;
-    const int blocks256 = (sets + (256 / pl.lpr) - 1) / (256 / pl.lpr);
-    pl.bt = blocks256 >= 4 * cu_count() ? 256 : 64;
+    pl.bt = 256;
     return pl;
 }
 
@@ -468,10 +521,12 @@ void launch_fast(const GemvParams& p, hipStream_t s) {
     constexpr int SEGS = BT / LPR;
     const int sets = (p.n_rows + RPS - 1) / RPS;
     int grid = (sets + SEGS - 1) / SEGS;
-    const int cap = cu_count() * (BT == 256 ? 4 : 8);
-    if (grid > cap) grid = cap;
-    const size_t lds = XM == kXQ8 ? 0 : static_cast<size_t>(p.K) + (p.K >> 5) * 8;
-    gemv_w4_kernel<BT, LPR, NCH, RPS, MODE, XM><<<grid, BT, lds, s>>>(p);
+    const int cap = cu_count() * 8;
+    const size_t lds = static_cast<size_t>(p.K) + (p.K >> 5) * 8 + 32;  // + dummy slot
+    if (grid > cap)
+        gemv_w4_kernel<BT, LPR, NCH, RPS, MODE, XM, true><<<cap, BT, lds, s>>>(p);
+    else
+        gemv_w4_kernel<BT, LPR, NCH, RPS, MODE, XM, false><<<grid, BT, lds, s>>>(p);
 }
 
 template <int MODE, int XM, int BT, int RPS>
@@ -482,7 +537,7 @@ bool dispatch_chunks(const Plan& pl, const GemvParams& p, hipStream_t s) {
             case 3: launch_fast<MODE, XM, BT, 16, 3, RPS>(p, s); return true;
             case 6: launch_fast<MODE, XM, BT, 16, 6, RPS>(p, s); return true;
         }
-    } else {
+    } else if constexpr (!(MODE == kSwiglu && RPS == 1)) {
         switch (pl.nch) {
             case 3: launch_fast<MODE, XM, BT, 64, 3, RPS>(p, s); return true;
             case 5: launch_fast<MODE, XM, BT, 64, 5, RPS>(p, s); return true;
@@ -494,21 +549,11 @@ bool dispatch_chunks(const Plan& pl, const GemvParams& p, hipStream_t s) {
 
 template <int MODE, int XM>
 bool dispatch_fast(const Plan& pl, const GemvParams& p, hipStream_t s) {
-    if constexpr (XM != kXQ8) {  // fp16 activations are staged by 256-thread blocks
-        if constexpr (MODE == kSwiglu) {
-            return dispatch_chunks<MODE, XM, 256, 2>(pl, p, s);
-        } else {
-            return pl.rps == 2 ? dispatch_chunks<MODE, XM, 256, 2>(pl, p, s)
-                               : dispatch_chunks<MODE, XM, 256, 1>(pl, p, s);
-        }
-    } else if constexpr (MODE == kSwiglu) {
-        return pl.bt == 256 ? dispatch_chunks<MODE, XM, 256, 2>(pl, p, s) : dispatch_chunks<MODE, XM, 64, 2>(pl, p, s);
-    } else {
-        if (pl.rps == 2)
-            return pl.bt == 256 ? dispatch_chunks<MODE, XM, 256, 2>(pl, p, s)
-                                : dispatch_chunks<MODE, XM, 64, 2>(pl, p, s);
-        return pl.bt == 256 ? dispatch_chunks<MODE, XM, 256, 1>(pl, p, s) : dispatch_chunks<MODE, XM, 64, 1>(pl, p, s);
+    if (pl.rps == 2) {
+        if constexpr (MODE == kSwiglu) return dispatch_chunks<MODE, XM, 256, 2>(pl, p, s);
+        return false;
     }
+    return dispatch_chunks<MODE, XM, 256, 1>(pl, p, s);
 }
 
 template <int MODE, int XM>
@@ -518,7 +563,10 @@ int launch_gemv(GemvParams& p, bool fast_ok, hipStream_t stream, const char* wha
     if (fast_ok && K <= kMaxFastK) {
         const Plan pl = plan_for(K, p.n_rows, MODE, XM != kXQ8);
         bool qkv_ok = true;
-        if (MODE == kQKV && pl.rps == 2) qkv_ok = (p.row_begin[1] % 2 == 0) && (p.row_begin[2] % 2 == 0);
+        if (MODE == kQKV) {  // matrix boundaries on whole blocks (row_ptrs)
+            const int rows_per_block = 256 / pl.lpr * pl.rps;
+            qkv_ok = (p.row_begin[1] % rows_per_block == 0) && (p.row_begin[2] % rows_per_block == 0);
+        }
         if (qkv_ok) {
             if (!dispatch_fast<MODE, XM>(pl, p, stream))
                 return fail(QE_ERR_UNSUPPORTED, "%s: no kernel for K=%d", what, K);
