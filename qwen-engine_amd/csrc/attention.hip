@@ -16,7 +16,6 @@ namespace {
 
 constexpr int kSplits = 16;   // FLASH_DECODE_SPLITS, include/config.cuh:29
 constexpr int kHeadDim = 128;
-constexpr int kMaxGroup = 8;  // q heads per kv head handled by stage 1
 constexpr int kVocab = 151936;  // VOCAB_SIZE: out-of-range token ids map to 0
 
 __device__ __forceinline__ float2 h2f2(uint32_t w) {
@@ -43,6 +42,11 @@ __global__ __launch_bounds__(256) void embed_lookup_w4a16_kernel(const uint32_t*
 }
 
 // ---- QKV bias + NeoX RoPE + KV append ------------------------------------------
+// grid (tokens, ceil((nq + nkv) / 2)), 256 threads: thread (hl, e) owns
+// element e of head 2*blockIdx.y + hl of the combined [q heads, k heads]
+// list; threads of a k head also own element e of the matching v head.
+// Every operand is loaded once up front, one barrier separates the reads
+// of the rotation partner from the in-place writes.
 __global__ __launch_bounds__(256) void qkv_bias_rope_kv_append_kernel(
     uint16_t* __restrict__ q, uint16_t* __restrict__ k, uint16_t* __restrict__ v, const uint16_t* __restrict__ qb,
     const uint16_t* __restrict__ kb, const uint16_t* __restrict__ vb, uint16_t* __restrict__ kc,
@@ -51,49 +55,193 @@ __global__ __launch_bounds__(256) void qkv_bias_rope_kv_append_kernel(
     const int m = blockIdx.x;
     int pos = ctl != nullptr ? ctl->seq_pos + m : 0;
     if (pos >= max_seq) pos = max_seq - 1;
+    const int per_block = blockDim.x / hd;  // heads per block (hd <= 256)
+    const int hl = threadIdx.x / hd, e = threadIdx.x % hd;
+    const int head = blockIdx.y * per_block + hl;
+    const bool live = hl < per_block && head < nq + nkv;
+    const bool is_k = head >= nq;
     const int q_dim = nq * hd, kv_dim = nkv * hd;
-    _Float16* qm = reinterpret_cast<_Float16*>(q + static_cast<size_t>(m) * q_dim);
-    _Float16* km = reinterpret_cast<_Float16*>(k + static_cast<size_t>(m) * kv_dim);
-    _Float16* vm = reinterpret_cast<_Float16*>(v + static_cast<size_t>(m) * kv_dim);
-    // 1. bias (fp16 adds)
-    for (int i = threadIdx.x; i < q_dim; i += blockDim.x)
-        if (qb) qm[i] = qm[i] + __builtin_bit_cast(_Float16, qb[i]);
-    for (int i = threadIdx.x; i < kv_dim; i += blockDim.x) {
-        if (kb) km[i] = km[i] + __builtin_bit_cast(_Float16, kb[i]);
-        if (vb) vm[i] = vm[i] + __builtin_bit_cast(_Float16, vb[i]);
-    }
-    __syncthreads();
-    // 2. rotate pairs (i, i + rot/2) of the first rot elements of each q/k head
     const int rot = (rotary_dim > 0 && rotary_dim <= hd) ? rotary_dim : hd;
     const int half_rot = rot / 2;
-    const float log2_theta = log2f(rope_theta);
-    const int pairs = (nq + nkv) * half_rot;
-    for (int pi = threadIdx.x; pi < pairs; pi += blockDim.x) {
-        const int head = pi / half_rot;
-        const int i = pi % half_rot;
-        const float inv_freq = exp2f(-2.0f * static_cast<float>(i) / static_cast<float>(rot) * log2_theta);
+    const int pe = e < rot ? (e < half_rot ? e + half_rot : e - half_rot) : e;  // rotation partner
+    _Float16* hp = nullptr;
+    const uint16_t* bp = nullptr;
+    if (live) {
+        hp = is_k ? reinterpret_cast<_Float16*>(k + static_cast<size_t>(m) * kv_dim + (head - nq) * hd)
+                  : reinterpret_cast<_Float16*>(q + static_cast<size_t>(m) * q_dim + head * hd);
+        bp = is_k ? (kb ? kb + (head - nq) * hd : nullptr) : (qb ? qb + head * hd : nullptr);
+    }
+    _Float16 xe = 0, xp = 0, ve = 0;
+    if (live) {
+        xe = hp[e];
+        xp = hp[pe];
+        if (bp) {  // bias added in fp16 (rounded) before the rotation
+            xe = xe + __builtin_bit_cast(_Float16, bp[e]);
+            xp = xp + __builtin_bit_cast(_Float16, bp[pe]);
+        }
+        if (is_k) {
+            const size_t vo = static_cast<size_t>(m) * kv_dim + (head - nq) * hd + e;
+            ve = __builtin_bit_cast(_Float16, v[vo]);
+            if (vb) ve = ve + __builtin_bit_cast(_Float16, vb[(head - nq) * hd + e]);
+        }
+    }
+    float outv = static_cast<float>(xe);
+    if (e < rot) {
+        const int i = e < half_rot ? e : e - half_rot;
+        const float inv_freq = exp2f(-2.0f * static_cast<float>(i) / static_cast<float>(rot) * log2f(rope_theta));
         float sn, cs;
         sincosf(static_cast<float>(pos) * inv_freq, &sn, &cs);
-        _Float16* hp = head < nq ? qm + head * hd : km + (head - nq) * hd;
-        const float x0 = static_cast<float>(hp[i]);
-        const float x1 = static_cast<float>(hp[i + half_rot]);
-        hp[i] = static_cast<_Float16>(x0 * cs - x1 * sn);
-        hp[i + half_rot] = static_cast<_Float16>(x0 * sn + x1 * cs);
+        const float x = static_cast<float>(xe), y = static_cast<float>(xp);
+        outv = e < half_rot ? x * cs - y * sn : y * sn + x * cs;  // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
     }
-    __syncthreads();
-    // 3. append rotated k and biased v at position pos
-    for (int i = threadIdx.x; i < kv_dim; i += blockDim.x) {
-        const int head = i / hd, d = i % hd;
-        const size_t off = (static_cast<size_t>(head) * max_seq + pos) * hd + d;
-        kc[off] = __builtin_bit_cast(uint16_t, km[i]);
-        vc[off] = __builtin_bit_cast(uint16_t, vm[i]);
+    __syncthreads();  // partners read before anyone writes
+    if (!live) return;
+    const _Float16 o = static_cast<_Float16>(outv);
+    hp[e] = o;
+    if (is_k) {
+        const size_t co = (static_cast<size_t>(head - nq) * max_seq + pos) * hd + e;
+        kc[co] = __builtin_bit_cast(uint16_t, o);
+        v[static_cast<size_t>(m) * kv_dim + (head - nq) * hd + e] = __builtin_bit_cast(uint16_t, ve);
+        vc[co] = __builtin_bit_cast(uint16_t, ve);
     }
 }
 
 // ---- flash decode, stage 1 -----------------------------------------------------
-// grid (num_kv_heads, kSplits), 256 threads (4 waves).  Wave w walks tokens
-// split_start + w, +4, ...; lane l holds dims 2l, 2l+1 of every q head of
-// the group.  Writes unnormalized partial outputs and (max, denominator).
+// grid (num_kv_heads, kSplits), 256 threads.  A split is a contiguous run
+// of at most 256 positions.  Each wave takes 4 positions per step, one per
+// 16-lane group; lane j of a group holds dims 8j..8j+7 (one 16-byte K and V
+// load per position), so a score is a 16-lane DPP sum.  K and V rows of
+// four steps (64 positions per block) are requested before any of them is
+// used.  Online softmax per lane group in the exp2 domain; the 4 groups and
+// 4 waves are merged at the end.  Output per (q head, split): unnormalized
+// o relative to the split max m, and (m, denominator) with m in natural-log
+// units, as attention_gqa.cu's stage 1 writes them.
+constexpr int kRound = 4;  // wave steps per round of loads
+
+__device__ __forceinline__ void unpack8_f32(const u32x4 w, float (&f)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = h2f(static_cast<uint16_t>(w[i] & 0xFFFFu));
+        f[2 * i + 1] = h2f(static_cast<uint16_t>(w[i] >> 16));
+    }
+}
+
+template <int GROUP>
+__device__ __forceinline__ void flash_decode_split(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                   const uint16_t* __restrict__ vc, float* __restrict__ part_o,
+                                                   float* __restrict__ part_lse, int kvh, int split, int t0, int t1,
+                                                   int max_seq) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15;
+    const int qh0 = kvh * GROUP;
+    constexpr float kLog2e = 1.4426950408889634f;
+    const float sc2 = kLog2e / sqrtf(static_cast<float>(kHeadDim));  // scores scaled into the exp2 domain
+    float qf[GROUP][8];
+#pragma unroll
+    for (int h = 0; h < GROUP; ++h) {
+        float f[8];
+        unpack8_f32(*reinterpret_cast<const u32x4*>(q + (qh0 + h) * kHeadDim + 8 * j), f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[h][i] = f[i] * sc2;
+    }
+    float mh[GROUP], lh[GROUP], oh[GROUP][8];
+#pragma unroll
+    for (int h = 0; h < GROUP; ++h) {
+        mh[h] = -INFINITY;
+        lh[h] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) oh[h][i] = 0.0f;
+    }
+    const size_t base = static_cast<size_t>(kvh) * max_seq * kHeadDim + 8 * j;
+    for (int r0 = t0; r0 < t1; r0 += 64) {
+        u32x4 kr[kRound], vr[kRound];
+#pragma unroll
+        for (int st = 0; st < kRound; ++st) {
+            const int t = min(r0 + st * 16 + wave * 4 + g, t1 - 1);
+            kr[st] = *reinterpret_cast<const u32x4*>(kc + base + static_cast<size_t>(t) * kHeadDim);
+            vr[st] = *reinterpret_cast<const u32x4*>(vc + base + static_cast<size_t>(t) * kHeadDim);
+        }
+        const int steps = min(kRound, (t1 - r0 + 15) / 16);  // block-uniform: skip empty steps
+#pragma unroll
+        for (int st = 0; st < kRound; ++st) {
+            if (st >= steps) break;
+            const bool valid = r0 + st * 16 + wave * 4 + g < t1;
+            float kf[8], vf[8];
+            unpack8_f32(kr[st], kf);
+            unpack8_f32(vr[st], vf);
+#pragma unroll
+            for (int h = 0; h < GROUP; ++h) {
+                float d = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) d += qf[h][i] * kf[i];
+                const float sc = qwen::seg_sum<16>(d);
+                const float mn = valid ? fmaxf(mh[h], sc) : mh[h];
+                const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mh[h] - mn);
+                const float p = valid ? __builtin_amdgcn_exp2f(sc - mn) : 0.0f;
+                lh[h] = lh[h] * alpha + p;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) oh[h][i] = oh[h][i] * alpha + p * vf[i];
+                mh[h] = mn;
+            }
+        }
+    }
+    // merge the 4 lane groups of the wave (lanes j, j+16, j+32, j+48)
+#pragma unroll
+    for (int h = 0; h < GROUP; ++h) {
+#pragma unroll
+        for (int sh = 0; sh < 2; ++sh) {
+            const float mo = sh == 0 ? qwen::swz_xor16_f32(mh[h]) : __shfl_xor(mh[h], 32);
+            const float lo = sh == 0 ? qwen::swz_xor16_f32(lh[h]) : __shfl_xor(lh[h], 32);
+            const float mn = fmaxf(mh[h], mo);
+            const float a = mh[h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mh[h] - mn);
+            const float b = mo == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mn);
+            lh[h] = lh[h] * a + lo * b;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float oo = sh == 0 ? qwen::swz_xor16_f32(oh[h][i]) : __shfl_xor(oh[h][i], 32);
+                oh[h][i] = oh[h][i] * a + oo * b;
+            }
+            mh[h] = mn;
+        }
+    }
+    // merge the 4 waves through LDS; wave 0 writes
+    __shared__ float s_ml[4][GROUP][2];
+    __shared__ float s_o[4][GROUP][kHeadDim];
+    if (lane < 16) {
+#pragma unroll
+        for (int h = 0; h < GROUP; ++h) {
+            if (lane == 0) {
+                s_ml[wave][h][0] = mh[h];
+                s_ml[wave][h][1] = lh[h];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s_o[wave][h][8 * j + i] = oh[h][i];
+        }
+    }
+    __syncthreads();
+    // thread (h, d) for h < GROUP, d < 128: 2 elements per thread over 256 threads
+    constexpr float kLn2 = 0.6931471805599453f;
+    for (int idx = threadIdx.x; idx < GROUP * kHeadDim; idx += 256) {
+        const int h = idx / kHeadDim, d = idx % kHeadDim;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_ml[w][h][0]);
+        float lt = 0.0f, o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float f = s_ml[w][h][0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_ml[w][h][0] - mx);
+            lt += s_ml[w][h][1] * f;
+            o += s_o[w][h][d] * f;
+        }
+        const size_t row = static_cast<size_t>(qh0 + h) * kSplits + split;
+        part_o[row * kHeadDim + d] = o;
+        if (d == 0) {
+            part_lse[row * 2] = mx * kLn2;  // natural-log units
+            part_lse[row * 2 + 1] = lt;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void flash_decode_stage1_kernel(const uint16_t* __restrict__ q,
                                                                   const uint16_t* __restrict__ kc,
                                                                   const uint16_t* __restrict__ vc,
@@ -108,90 +256,27 @@ __global__ __launch_bounds__(256) void flash_decode_stage1_kernel(const uint16_t
     const int per = (seq_len + kSplits - 1) / kSplits;
     const int t0 = split * per;
     const int t1 = min(t0 + per, seq_len);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int qh0 = kvh * group;
     if (t0 >= t1) {
         if (threadIdx.x < group) {
-            const size_t li = (static_cast<size_t>(qh0 + threadIdx.x) * kSplits + split) * 2;
+            const size_t li = (static_cast<size_t>(kvh * group + threadIdx.x) * kSplits + split) * 2;
             part_lse[li] = -INFINITY;
             part_lse[li + 1] = 0.0f;
         }
         return;
     }
-    float2 qv[kMaxGroup];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h)
-        qv[h] = h < group ? h2f2(reinterpret_cast<const uint32_t*>(q + (qh0 + h) * kHeadDim)[lane]) : make_float2(0, 0);
-    float mi[kMaxGroup], di[kMaxGroup];
-    float2 oi[kMaxGroup];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) {
-        mi[h] = -INFINITY;
-        di[h] = 0.0f;
-        oi[h] = make_float2(0.0f, 0.0f);
-    }
-    const float scale = 1.0f / sqrtf(static_cast<float>(kHeadDim));
-    const size_t base = static_cast<size_t>(kvh) * max_seq * kHeadDim;
-    for (int t = t0 + wave; t < t1; t += 4) {
-        const float2 kv = h2f2(reinterpret_cast<const uint32_t*>(kc + base + static_cast<size_t>(t) * kHeadDim)[lane]);
-        const float2 vv = h2f2(reinterpret_cast<const uint32_t*>(vc + base + static_cast<size_t>(t) * kHeadDim)[lane]);
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h) {
-            if (h < group) {
-                const float s = qwen::seg_sum<64>(qv[h].x * kv.x + qv[h].y * kv.y) * scale;
-                const float mc = fmaxf(mi[h], s);
-                const float alpha = expf(mi[h] - mc);
-                const float beta = expf(s - mc);
-                di[h] = di[h] * alpha + beta;
-                oi[h].x = oi[h].x * alpha + beta * vv.x;
-                oi[h].y = oi[h].y * alpha + beta * vv.y;
-                mi[h] = mc;
-            }
-        }
-    }
-    __shared__ float s_m[kMaxGroup][4], s_d[kMaxGroup][4];
-    __shared__ float2 s_o[4][kMaxGroup][64];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) {
-        if (h < group) {
-            if (lane == 0) {
-                s_m[h][wave] = mi[h];
-                s_d[h][wave] = di[h];
-            }
-            s_o[wave][h][lane] = oi[h];
-        }
-    }
-    __syncthreads();
-    // merge the 4 waves: thread (h, lane) for h = wave, wave + 4
-    for (int h = wave; h < group; h += 4) {
-        float mmax = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < 4; ++w)
-            if (s_d[h][w] > 0.0f) mmax = fmaxf(mmax, s_m[h][w]);
-        float dt = 0.0f;
-        float2 o = make_float2(0.0f, 0.0f);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            if (s_d[h][w] > 0.0f) {
-                const float f = expf(s_m[h][w] - mmax);
-                dt += s_d[h][w] * f;
-                o.x += f * s_o[w][h][lane].x;
-                o.y += f * s_o[w][h][lane].y;
-            }
-        }
-        const size_t oi_ = (static_cast<size_t>(qh0 + h) * kSplits + split) * kHeadDim + 2 * lane;
-        part_o[oi_] = dt > 0.0f ? o.x : 0.0f;
-        part_o[oi_ + 1] = dt > 0.0f ? o.y : 0.0f;
-        if (lane == 0) {
-            const size_t li = (static_cast<size_t>(qh0 + h) * kSplits + split) * 2;
-            part_lse[li] = mmax;
-            part_lse[li + 1] = dt;
-        }
+    switch (group) {  // q heads per kv head: compile-time so every array stays in VGPRs
+        case 1: flash_decode_split<1>(q, kc, vc, part_o, part_lse, kvh, split, t0, t1, max_seq); break;
+        case 2: flash_decode_split<2>(q, kc, vc, part_o, part_lse, kvh, split, t0, t1, max_seq); break;
+        case 4: flash_decode_split<4>(q, kc, vc, part_o, part_lse, kvh, split, t0, t1, max_seq); break;
+        case 6: flash_decode_split<6>(q, kc, vc, part_o, part_lse, kvh, split, t0, t1, max_seq); break;
+        case 8: flash_decode_split<8>(q, kc, vc, part_o, part_lse, kvh, split, t0, t1, max_seq); break;
+        default: break;  // rejected on the host
     }
 }
 
 // ---- flash decode, stage 2 + Q8_1 epilogue ---------------------------------------
-// grid num_q_heads, 128 threads (one per element of the head).
+// grid num_q_heads, 128 threads (one per element of the head).  Every
+// thread loads the 16 (m, d) pairs and its 16 partials up front.
 // acc = sum_s exp(m_s - m) / d * o_s; attn_out = fp16(acc).  Epilogue
 // (attention_gqa.cu:263-310): d = max(max|acc|/127, 1e-8) per head (= one
 // 128-group), q = clamp(rint(acc / d)), sum8 over 8 adjacent elements.
@@ -201,39 +286,36 @@ __global__ __launch_bounds__(128) void flash_decode_stage2_kernel(const float* _
                                                                   int8_t* __restrict__ q8, float* __restrict__ q_scale,
                                                                   int32_t* __restrict__ q_sum8) {
     const int qh = blockIdx.x, tid = threadIdx.x;
-    __shared__ float s_m[kSplits], s_d[kSplits];
-    __shared__ float s_mg, s_dg;
-    __shared__ float s_wmax[2];
-    if (tid < kSplits) {
-        const size_t li = (static_cast<size_t>(qh) * kSplits + tid) * 2;
-        s_m[tid] = part_lse[li];
-        s_d[tid] = part_lse[li + 1];
+    float ms[kSplits], ds[kSplits], os[kSplits];
+#pragma unroll
+    for (int s = 0; s < kSplits; ++s) {
+        const size_t row = static_cast<size_t>(qh) * kSplits + s;
+        const float2 ml = *reinterpret_cast<const float2*>(part_lse + row * 2);
+        ms[s] = ml.x;
+        ds[s] = ml.y;
+        os[s] = part_o[row * kHeadDim + tid];
     }
-    __syncthreads();
-    if (tid == 0) {
-        float mg = -INFINITY;
-        for (int s = 0; s < kSplits; ++s)
-            if (s_d[s] > 0.0f) mg = fmaxf(mg, s_m[s]);
-        float dg = 0.0f;
-        for (int s = 0; s < kSplits; ++s)
-            if (s_d[s] > 0.0f) dg += s_d[s] * expf(s_m[s] - mg);
-        s_mg = mg;
-        s_dg = dg;
+    float mg = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kSplits; ++s)
+        if (ds[s] > 0.0f) mg = fmaxf(mg, ms[s]);
+    constexpr float kLog2e = 1.4426950408889634f;
+    float es[kSplits];  // exp(m_s - m), hardware exp2
+    float dg = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kSplits; ++s) {
+        es[s] = ds[s] > 0.0f ? __builtin_amdgcn_exp2f((ms[s] - mg) * kLog2e) : 0.0f;
+        dg += ds[s] * es[s];
     }
-    __syncthreads();
-    const float mg = s_mg, dg = s_dg;
     float acc = 0.0f;
     if (dg > 0.0f) {
         const float inv = 1.0f / dg;
-        for (int s = 0; s < kSplits; ++s) {
-            if (s_d[s] > 0.0f) {
-                const float wgt = expf(s_m[s] - mg) * inv;
-                acc += wgt * part_o[(static_cast<size_t>(qh) * kSplits + s) * kHeadDim + tid];
-            }
-        }
+#pragma unroll
+        for (int s = 0; s < kSplits; ++s) acc += ds[s] > 0.0f ? es[s] * inv * os[s] : 0.0f;  // empty splits hold no partials
     }
     attn_out[static_cast<size_t>(qh) * kHeadDim + tid] = f2h(acc);
     if (q8 == nullptr) return;  // uniform across the block
+    __shared__ float s_wmax[2];
     float mx = qwen::seg_max<64>(fabsf(acc));
     if ((tid & 63) == 0) s_wmax[tid >> 6] = mx;
     __syncthreads();
@@ -354,7 +436,10 @@ extern "C" int qe_launch_qkv_bias_rope_kv_append(uint16_t* q, uint16_t* k, uint1
     QE_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && max_seq_len > 0,
                "qkv_bias_rope_kv_append: bad head shape");
     if (num_tokens <= 0) return QE_OK;
-    qkv_bias_rope_kv_append_kernel<<<num_tokens, 256, 0, stream>>>(q, k, v, q_bias, k_bias, v_bias, layer_k_cache,
+    QE_REQUIRE(head_dim <= 256, "qkv_bias_rope_kv_append: head_dim=%d > 256", head_dim);
+    const int heads_per_block = 256 / head_dim;
+    const dim3 grid(num_tokens, (num_q_heads + num_kv_heads + heads_per_block - 1) / heads_per_block);
+    qkv_bias_rope_kv_append_kernel<<<grid, 256, 0, stream>>>(q, k, v, q_bias, k_bias, v_bias, layer_k_cache,
                                                                    layer_v_cache, d_control, num_q_heads,
                                                                    num_kv_heads, head_dim, max_seq_len,
                                                                    rotary_dim, rope_theta);
@@ -371,8 +456,11 @@ extern "C" int qe_launch_attention_gqa_flash_decode(const uint16_t* q, const uin
     QE_REQUIRE(q && layer_k_cache && layer_v_cache && splitk_partial_out && splitk_partial_lse && attn_out,
                "attention_gqa_flash_decode: NULL pointer");
     QE_REQUIRE(head_dim == kHeadDim, "attention_gqa_flash_decode: head_dim=%d (only 128 is built)", head_dim);
-    QE_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && num_q_heads / num_kv_heads <= kMaxGroup,
+    QE_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
                "attention_gqa_flash_decode: %d q heads over %d kv heads", num_q_heads, num_kv_heads);
+    const int group = num_q_heads / num_kv_heads;
+    QE_REQUIRE(group == 1 || group == 2 || group == 4 || group == 6 || group == 8,
+               "attention_gqa_flash_decode: %d q heads per kv head (built: 1, 2, 4, 6, 8)", group);
     QE_REQUIRE(max_seq_len > 0, "attention_gqa_flash_decode: max_seq_len=%d", max_seq_len);
     flash_decode_stage1_kernel<<<dim3(num_kv_heads, kSplits), 256, 0, stream>>>(
         q, layer_k_cache, layer_v_cache, splitk_partial_out, splitk_partial_lse, d_control, num_q_heads, num_kv_heads,

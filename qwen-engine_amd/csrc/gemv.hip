@@ -511,8 +511,11 @@ Plan plan_for(int K, int n_rows, int mode, bool f16_input) {
     // segments); 64-lane SwiGLU segments own a row pair
     pl.rps = (mode == kSwiglu && pl.lpr == 64) ? 2 : 1;
     (void)n_rows;
-    (void)f16_input;
-    pl.bt = 256;
+    // fp16 input over long rows (K = 8960): 512-thread blocks halve the
+    // per-thread share of the in-block quantization, which is on the
+    // critical path; 256 everywhere else (measured on MI355X)
+    pl.bt = (f16_input && pl.lpr == 64) ? 512 : 256;
+    if (const int f = gemv_forced_bt()) pl.bt = f;
     return pl;
 }
 
@@ -521,7 +524,7 @@ void launch_fast(const GemvParams& p, hipStream_t s) {
     constexpr int SEGS = BT / LPR;
     const int sets = (p.n_rows + RPS - 1) / RPS;
     int grid = (sets + SEGS - 1) / SEGS;
-    const int cap = cu_count() * 8;
+    const int cap = cu_count() * 8 * 256 / BT;
     const size_t lds = static_cast<size_t>(p.K) + (p.K >> 5) * 8 + 32;  // + dummy slot
     if (grid > cap)
         gemv_w4_kernel<BT, LPR, NCH, RPS, MODE, XM, true><<<cap, BT, lds, s>>>(p);
@@ -547,13 +550,22 @@ bool dispatch_chunks(const Plan& pl, const GemvParams& p, hipStream_t s) {
     return false;
 }
 
-template <int MODE, int XM>
-bool dispatch_fast(const Plan& pl, const GemvParams& p, hipStream_t s) {
+template <int MODE, int XM, int BT>
+bool dispatch_rps(const Plan& pl, const GemvParams& p, hipStream_t s) {
     if (pl.rps == 2) {
-        if constexpr (MODE == kSwiglu) return dispatch_chunks<MODE, XM, 256, 2>(pl, p, s);
+        if constexpr (MODE == kSwiglu) return dispatch_chunks<MODE, XM, BT, 2>(pl, p, s);
         return false;
     }
-    return dispatch_chunks<MODE, XM, 256, 1>(pl, p, s);
+    return dispatch_chunks<MODE, XM, BT, 1>(pl, p, s);
+}
+
+template <int MODE, int XM>
+bool dispatch_fast(const Plan& pl, const GemvParams& p, hipStream_t s) {
+    switch (pl.bt) {
+        case 512: return dispatch_rps<MODE, XM, 512>(pl, p, s);
+        case 1024: return dispatch_rps<MODE, XM, 1024>(pl, p, s);
+        default: return dispatch_rps<MODE, XM, 256>(pl, p, s);
+    }
 }
 
 template <int MODE, int XM>
@@ -564,7 +576,7 @@ int launch_gemv(GemvParams& p, bool fast_ok, hipStream_t stream, const char* wha
         const Plan pl = plan_for(K, p.n_rows, MODE, XM != kXQ8);
         bool qkv_ok = true;
         if (MODE == kQKV) {  // matrix boundaries on whole blocks (row_ptrs)
-            const int rows_per_block = 256 / pl.lpr * pl.rps;
+            const int rows_per_block = pl.bt / pl.lpr * pl.rps;
             qkv_ok = (p.row_begin[1] % rows_per_block == 0) && (p.row_begin[2] % rows_per_block == 0);
         }
         if (qkv_ok) {
