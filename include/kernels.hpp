@@ -169,6 +169,32 @@ inline void launch_sample_and_advance(const half* logits, float* sample_scratch_
 }
 
 // ---- fused decode launchers of this build (no counterpart in kernels.cuh) ----
+inline void launch_gemv_lm_head_sample_w4a8(const uint32_t* qweight, const half* scales, const int8_t* input_q8,
+                                            const float* input_scale, const int32_t* input_sum8, half* logits_opt,
+                                            float* sample_scratch_val, int32_t* sample_scratch_idx,
+                                            DeviceControlBlock* d_control, int32_t* d_mapped_pinned_token,
+                                            hipStream_t stream, int vocab_size = VOCAB_SIZE,
+                                            int in_features = HIDDEN_SIZE) {
+    detail::check(qe_launch_gemv_lm_head_sample_w4a8(qweight, detail::h(scales), input_q8, input_scale, input_sum8,
+                                                     detail::h(logits_opt), sample_scratch_val, sample_scratch_idx,
+                                                     d_control, d_mapped_pinned_token, vocab_size, in_features,
+                                                     stream),
+                  "launch_gemv_lm_head_sample_w4a8");
+}
+
+inline void launch_rmsnorm_gemv_lm_head_sample_w4a16(const half* input, const half* gamma, half* output_fp16_opt,
+                                                     const uint32_t* qweight, const half* scales, half* logits_opt,
+                                                     float* sample_scratch_val, int32_t* sample_scratch_idx,
+                                                     DeviceControlBlock* d_control, int32_t* d_mapped_pinned_token,
+                                                     hipStream_t stream, int vocab_size = VOCAB_SIZE,
+                                                     int hidden_size = HIDDEN_SIZE) {
+    detail::check(qe_launch_rmsnorm_gemv_lm_head_sample_w4a16(
+                      detail::h(input), detail::h(gamma), detail::h(output_fp16_opt), qweight, detail::h(scales),
+                      detail::h(logits_opt), sample_scratch_val, sample_scratch_idx, d_control,
+                      d_mapped_pinned_token, vocab_size, hidden_size, stream),
+                  "launch_rmsnorm_gemv_lm_head_sample_w4a16");
+}
+
 inline void launch_rmsnorm_gemv_qkv_w4a16(const half* input, const half* gamma, half* output_fp16_opt,
                                           const QKVProjectionView& view, hipStream_t stream,
                                           int hidden_size = HIDDEN_SIZE, int num_q_heads = NUM_Q_HEADS,

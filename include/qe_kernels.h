@@ -151,15 +151,47 @@ int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_qwe
 
 /* ---- greedy sampling ------------------------------------------------------ */
 
-/* Replaces launch_sample_and_advance, include/kernels.cuh:209-217, for
- * greedy decoding: argmax over fp16 logits with the lowest index on ties
- * (NaN never wins), then token_id = winner, seq_pos += 1, rng_seed += the
- * reference's golden-ratio step.  sample_scratch_val/idx hold >= 256
- * entries.  The control block's temperature is ignored: Gumbel sampling is
- * not part of this build. */
+/* Replaces launch_sample_and_advance, include/kernels.cuh:209-217
+ * (src/kernels/sampling.cu:60-232): argmax over the fp16 logits, or, when
+ * the control block's temperature T > 1e-5, over logit / T plus Gumbel
+ * noise -log(-log(u)) with u from Philox-4x32-10 keyed by rng_seed at
+ * counter (index, seq_pos); lowest index on ties, NaN never wins; then
+ * token_id = winner, seq_pos += 1, rng_seed += 0x9E3779B97F4A7C15.
+ * sample_scratch_val/idx hold >= 256 entries. */
 int qe_launch_sample_and_advance(const uint16_t* logits, float* sample_scratch_val,
                                  int32_t* sample_scratch_idx, qe_device_control_block* d_control,
                                  int32_t* d_mapped_pinned_token, hipStream_t stream, int vocab_size);
+
+/* Partials written by the fused LM-head + sampling launches: the sample
+ * scratch of those two entry points holds at least this many entries (the
+ * reference's launch_sample_and_advance needs 256). */
+#define QE_LM_HEAD_SAMPLE_PARTS 2048
+
+/* LM-head GEMV fused with the first sampling stage, then the second stage:
+ * the same result as launch_gemv_w4a8 (logits, written when logits_opt is
+ * not NULL) followed by launch_sample_and_advance
+ * (src/engine.cu:437-447 -> src/kernels/sampling.cu:60-232), in two launches
+ * instead of three and without reading the logits back.  The compared value
+ * of index i is the fp16 logit, or logit / T + Gumbel(Philox(rng_seed, i,
+ * seq_pos)) when the control block's temperature T > 1e-5; ties keep the
+ * lowest index, NaN never wins; then token_id = winner, seq_pos += 1,
+ * rng_seed += 0x9E3779B97F4A7C15.  Needs 16-byte aligned weights and
+ * activations and in_features <= 16384 (QE_ERR_UNSUPPORTED otherwise). */
+int qe_launch_gemv_lm_head_sample_w4a8(const uint32_t* qweight, const uint16_t* scales, const int8_t* input_q8,
+                                       const float* input_scale, const int32_t* input_sum8, uint16_t* logits_opt,
+                                       float* sample_scratch_val, int32_t* sample_scratch_idx,
+                                       qe_device_control_block* d_control, int32_t* d_mapped_pinned_token,
+                                       int vocab_size, int in_features, hipStream_t stream);
+
+/* The same with the final RMSNorm (fp16 hidden state + gamma) quantized to
+ * Q8_1 inside the launch, replacing launch_rmsnorm_q8_1 + the above
+ * (src/engine.cu:433-447). */
+int qe_launch_rmsnorm_gemv_lm_head_sample_w4a16(const uint16_t* input, const uint16_t* gamma,
+                                                uint16_t* output_fp16_opt, const uint32_t* qweight,
+                                                const uint16_t* scales, uint16_t* logits_opt,
+                                                float* sample_scratch_val, int32_t* sample_scratch_idx,
+                                                qe_device_control_block* d_control, int32_t* d_mapped_pinned_token,
+                                                int vocab_size, int hidden_size, hipStream_t stream);
 
 /* ---- decode-loop kernels around the matrix path ---------------------------- */
 

@@ -387,6 +387,55 @@ int32_t oracle_argmax_f16(const uint16_t* logits, int n) {
 }
 
 // ---------------------------------------------------------------------------
+// Temperature sampling, src/kernels/sampling.cu:13-53 and :60-105: Philox-4x32-10
+// (Salmon et al., SC'11; multipliers 0xD2511F53 / 0xCD9E8D57, key bumps
+// 0x9E3779B9 / 0xBB67AE85) with counter (subsequence, offset, 0, 0) and key
+// (seed lo, seed hi); u = clamp((float(ctr0) + 1) / 4294967298.0f, 1e-7,
+// 1 - 1e-7); value = logit / temperature - log(-log(u)); argmax as greedy.
+// ---------------------------------------------------------------------------
+void oracle_philox4x32_10(const uint32_t ctr_in[4], const uint32_t key_in[2], uint32_t out[4]) {
+    uint32_t c0 = ctr_in[0], c1 = ctr_in[1], c2 = ctr_in[2], c3 = ctr_in[3];
+    uint32_t k0 = key_in[0], k1 = key_in[1];
+    for (int r = 0; r < 10; ++r) {
+        const uint64_t p0 = 0xD2511F53ull * c0;
+        const uint64_t p1 = 0xCD9E8D57ull * c2;
+        const uint32_t n0 = static_cast<uint32_t>(p1 >> 32) ^ c1 ^ k0;
+        const uint32_t n1 = static_cast<uint32_t>(p1);
+        const uint32_t n2 = static_cast<uint32_t>(p0 >> 32) ^ c3 ^ k1;
+        const uint32_t n3 = static_cast<uint32_t>(p0);
+        c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+float oracle_philox_uniform(uint64_t seed, uint32_t subsequence, uint32_t offset) {
+    const uint32_t ctr[4] = {subsequence, offset, 0u, 0u};
+    const uint32_t key[2] = {static_cast<uint32_t>(seed), static_cast<uint32_t>(seed >> 32)};
+    uint32_t o[4];
+    oracle_philox4x32_10(ctr, key, o);
+    const float u = (static_cast<float>(o[0]) + 1.0f) / 4294967298.0f;
+    return std::fmin(std::fmax(u, 1e-7f), 1.0f - 1e-7f);
+}
+
+int32_t oracle_sample_f16(const uint16_t* logits, int n, float temperature, uint64_t seed, uint32_t seq_pos,
+                          float* out_values) {
+    float best = -1e30f;
+    int32_t idx = 0;
+    for (int i = 0; i < n; ++i) {
+        float v = oracle_f16_to_f32(logits[i]);
+        if (temperature > 1e-5f) {
+            const float u = oracle_philox_uniform(seed, static_cast<uint32_t>(i), seq_pos);
+            v = v / temperature + -std::log(-std::log(u));
+        }
+        if (out_values) out_values[i] = v;
+        if (v > best) { best = v; idx = i; }
+    }
+    return idx;
+}
+
+// ---------------------------------------------------------------------------
 // Synthetic inputs.
 // ---------------------------------------------------------------------------
 // Generator of tests/test_kernels.cu:265-306 (libstdc++ distributions).

@@ -79,6 +79,16 @@ void oracle_rmsnorm_fp16(const uint16_t* x, const uint16_t* gamma, uint16_t* out
  * NaN never wins, floor -1e30 with default index 0. */
 int32_t oracle_argmax_f16(const uint16_t* logits, int n);
 
+/* Philox-4x32-10 block (10 rounds, key bumped after each round). */
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+/* Uniform of sampling.cu: counter (subsequence, offset, 0, 0), key = seed. */
+float oracle_philox_uniform(uint64_t seed, uint32_t subsequence, uint32_t offset);
+/* sample_stage1/2 of sampling.cu: Gumbel-max over logit/temperature when
+ * temperature > 1e-5, else greedy; out_values (optional) gets the compared
+ * value of every index. */
+int32_t oracle_sample_f16(const uint16_t* logits, int n, float temperature, uint64_t seed, uint32_t seq_pos,
+                          float* out_values);
+
 /* Inputs of the reference's synthetic SwiGLU suite (std::mt19937(42+H)):
  * x[H] fp16, qw[2I*H/8], scales[2I*H/128] fp16. */
 void oracle_suite3_inputs(int H, int I, uint16_t* x, uint32_t* qw, uint16_t* scales);

@@ -53,6 +53,7 @@ def lib():
             "oracle_gemm_swiglu_w4a16": [_P, _P, _P, _P, _I, _I, _I, _P, _P],
             "oracle_rmsnorm_fp16": [_P, _P, _P, _I, _I, ctypes.c_float],
             "oracle_argmax_f16": [_P, _I],
+            "oracle_philox4x32_10": [_P, _P, _P],
             "oracle_suite3_inputs": [_I, _I, _P, _P, _P],
             "oracle_synth_w4": [ctypes.c_uint64, _I, _I, _P, _P],
             "oracle_synth_f16_normal": [ctypes.c_uint64, _I64, _P],
@@ -62,6 +63,10 @@ def lib():
             fn.argtypes = args
             fn.restype = None
         L.oracle_argmax_f16.restype = ctypes.c_int32
+        L.oracle_philox_uniform.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32]
+        L.oracle_philox_uniform.restype = ctypes.c_float
+        L.oracle_sample_f16.argtypes = [_P, _I, ctypes.c_float, ctypes.c_uint64, ctypes.c_uint32, _P]
+        L.oracle_sample_f16.restype = ctypes.c_int32
         L.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.oracle_f16_to_f32.restype = ctypes.c_float
         L.oracle_f32_to_f16.argtypes = [ctypes.c_float]
@@ -236,6 +241,26 @@ def rmsnorm_fp16(x, gamma, eps=1e-6):
 def argmax_f16(logits) -> int:
     logits = _c(logits, np.float16)
     return int(lib().oracle_argmax_f16(_p(logits), logits.size))
+
+
+def philox4x32_10(ctr, key):
+    ctr = _c(np.asarray(ctr, np.uint32), np.uint32)
+    key = _c(np.asarray(key, np.uint32), np.uint32)
+    out = np.empty(4, np.uint32)
+    lib().oracle_philox4x32_10(_p(ctr), _p(key), _p(out))
+    return out
+
+
+def philox_uniform(seed: int, subsequence: int, offset: int) -> float:
+    return float(lib().oracle_philox_uniform(seed, subsequence, offset))
+
+
+def sample_f16(logits, temperature: float, seed: int, seq_pos: int):
+    """(token, compared values) of the reference's sample_and_advance."""
+    logits = _c(logits, np.float16)
+    vals = np.empty(logits.size, np.float32)
+    tok = int(lib().oracle_sample_f16(_p(logits), logits.size, temperature, seed, seq_pos, _p(vals)))
+    return tok, vals
 
 
 # -- synthetic inputs ----------------------------------------------------------

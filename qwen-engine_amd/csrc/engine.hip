@@ -218,6 +218,13 @@ int decode_pass(qe_engine* e, Timer* t) {
         }
         QE_TRY(mark(e, t, 0));
     }
+    if (c.fused_decode) {  // final RMSNorm + tied LM head + sampling stage 1, then stage 2 + advance
+        QE_TRY(qe_launch_rmsnorm_gemv_lm_head_sample_w4a16(e->act0, e->final_norm, nullptr, e->embed.w, e->embed.s,
+                                                           e->logits, e->sample_val, e->sample_idx, e->ctl,
+                                                           e->d_token, c.vocab_size, H, s));
+        QE_TRY(mark(e, t, 0));
+        return QE_OK;
+    }
     QE_TRY(qe_launch_rmsnorm_q8_1(e->act0, e->final_norm, nullptr, e->q8, e->q8_scale, e->q8_sum8, s, H));
     QE_TRY(mark(e, t, 2));
     QE_TRY(qe_launch_gemv_w4a8(e->embed.w, e->embed.s, e->q8, e->q8_scale, e->q8_sum8, nullptr, e->logits,
@@ -370,8 +377,8 @@ extern "C" int qe_engine_create(const qe_engine_config* cfg, uint64_t seed, qe_e
     e->q8_sum8 = e->take<int32_t>(QN / 8 * 4);
     e->part_o = e->take<float>(static_cast<size_t>(c.num_q_heads) * 16 * 128 * 4);
     e->part_lse = e->take<float>(static_cast<size_t>(c.num_q_heads) * 16 * 2 * 4);
-    e->sample_val = e->take<float>(256 * 4);
-    e->sample_idx = e->take<int32_t>(256 * 4);
+    e->sample_val = e->take<float>(QE_LM_HEAD_SAMPLE_PARTS * 4);
+    e->sample_idx = e->take<int32_t>(QE_LM_HEAD_SAMPLE_PARTS * 4);
     e->tokens = e->take<int32_t>(static_cast<size_t>(c.max_seq_len) * 4);
     e->ctl = e->take<qe_device_control_block>(sizeof(qe_device_control_block));
     QE_REQUIRE(e->arena_used <= e->arena_size, "engine_create: arena overflow (%zu > %zu)", e->arena_used,

@@ -26,7 +26,7 @@
 //     persistent blocks (grid capped per CU).
 // Shapes outside the fast kernel (weights not 16-byte aligned, K > 16384)
 // use a generic wave-per-row kernel that stages Q8_1 in LDS.
-#include "qe_common.hpp"
+#include "sample_common.hpp"
 
 namespace qe {
 namespace {
@@ -34,6 +34,7 @@ namespace {
 constexpr int kPlain = 0;
 constexpr int kQKV = 1;
 constexpr int kSwiglu = 2;
+constexpr int kSample = 3;  // LM head: plain rows, logits optional, (value, index) partial per block
 
 constexpr int kXQ8 = 0;   // Q8_1 activation
 constexpr int kXF16 = 1;  // fp16 activation, quantized in the block
@@ -53,6 +54,9 @@ struct GemvParams {
     const uint16_t* x16;    // fp16 activation (kXF16 / kXRMS)
     const uint16_t* gamma;  // RMSNorm weight (kXRMS)
     uint16_t* norm_out;     // optional fp16 normalized activation (kXRMS, block 0 writes)
+    float* s_val;           // kSample: per-block best value / index
+    int32_t* s_idx;
+    const qe_device_control_block* ctl;  // kSample: temperature, rng_seed, seq_pos
     int n_rows;             // physical weight rows
     int K;
 };
@@ -381,6 +385,17 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
     }
 
     // ---- row sets: one pass, or a grid-stride loop with the next set prefetched
+    float temp = 0.0f;
+    uint64_t seed = 0;
+    uint32_t seq_pos = 0;
+    if constexpr (MODE == kSample) {
+        if (p.ctl != nullptr) {
+            temp = p.ctl->temperature;
+            seed = p.ctl->rng_seed;
+            seq_pos = static_cast<uint32_t>(p.ctl->seq_pos);
+        }
+    }
+    Best best{-1e30f, 0};
     auto finish_set = [&](int st) __attribute__((always_inline)) {
         float acc[RPS];
 #pragma unroll
@@ -394,7 +409,12 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
         }
         if constexpr (PAIR) acc[0] = silu_mul(acc[0], qwen::swz_xor16_f32(acc[0]));  // gate (even set) x up
         if (l == 0 && st < n_sets) {
-            if constexpr (PAIR) {
+            if constexpr (MODE == kSample) {
+                const uint16_t logit = f2h(acc[0]);
+                if (p.out[0] != nullptr) p.out[0][st] = logit;
+                const float v = sample_value(h2f(logit), temp, seed, static_cast<uint32_t>(st), seq_pos);
+                best = better(best, Best{v, st});
+            } else if constexpr (PAIR) {
                 if ((st & 1) == 0) p.out[0][st >> 1] = f2h(acc[0]);
             } else if constexpr (MODE == kSwiglu) {
                 p.out[0][st] = f2h(silu_mul(acc[0], acc[1]));
@@ -432,6 +452,21 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
                     w[r][i] = wn[r][i];
                     hs[r][i] = hn[r][i];
                 }
+        }
+    }
+    if constexpr (MODE == kSample) {  // segment leaders -> one partial per block
+        __shared__ float s_bv[SEGS];
+        __shared__ int32_t s_bi[SEGS];
+        if (l == 0) {
+            s_bv[seg] = best.v;
+            s_bi[seg] = best.i;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            Best b{s_bv[0], s_bi[0]};
+            for (int g = 1; g < SEGS; ++g) b = better(b, Best{s_bv[g], s_bi[g]});
+            p.s_val[blockIdx.x] = b.v;
+            p.s_idx[blockIdx.x] = b.i;
         }
     }
 }
@@ -520,47 +555,50 @@ Plan plan_for(int K, int n_rows, int mode, bool f16_input) {
 }
 
 template <int MODE, int XM, int BT, int LPR, int NCH, int RPS>
-void launch_fast(const GemvParams& p, hipStream_t s) {
+int launch_fast(const GemvParams& p, hipStream_t s) {
     constexpr int SEGS = BT / LPR;
     const int sets = (p.n_rows + RPS - 1) / RPS;
     int grid = (sets + SEGS - 1) / SEGS;
-    const int cap = cu_count() * 8 * 256 / BT;
+    int cap = cu_count() * 8 * 256 / BT;
+    if (MODE == kSample && cap > QE_LM_HEAD_SAMPLE_PARTS) cap = QE_LM_HEAD_SAMPLE_PARTS;
     const size_t lds = static_cast<size_t>(p.K) + (p.K >> 5) * 8 + 32;  // + dummy slot
-    if (grid > cap)
+    if (grid > cap) {
         gemv_w4_kernel<BT, LPR, NCH, RPS, MODE, XM, true><<<cap, BT, lds, s>>>(p);
-    else
-        gemv_w4_kernel<BT, LPR, NCH, RPS, MODE, XM, false><<<grid, BT, lds, s>>>(p);
+        return cap;
+    }
+    gemv_w4_kernel<BT, LPR, NCH, RPS, MODE, XM, false><<<grid, BT, lds, s>>>(p);
+    return grid;
 }
 
 template <int MODE, int XM, int BT, int RPS>
-bool dispatch_chunks(const Plan& pl, const GemvParams& p, hipStream_t s) {
+int dispatch_chunks(const Plan& pl, const GemvParams& p, hipStream_t s) {
     if (pl.lpr == 16) {
         switch (pl.nch) {
-            case 2: launch_fast<MODE, XM, BT, 16, 2, RPS>(p, s); return true;
-            case 3: launch_fast<MODE, XM, BT, 16, 3, RPS>(p, s); return true;
-            case 6: launch_fast<MODE, XM, BT, 16, 6, RPS>(p, s); return true;
+            case 2: return launch_fast<MODE, XM, BT, 16, 2, RPS>(p, s);
+            case 3: return launch_fast<MODE, XM, BT, 16, 3, RPS>(p, s);
+            case 6: return launch_fast<MODE, XM, BT, 16, 6, RPS>(p, s);
         }
     } else if constexpr (!(MODE == kSwiglu && RPS == 1)) {
         switch (pl.nch) {
-            case 3: launch_fast<MODE, XM, BT, 64, 3, RPS>(p, s); return true;
-            case 5: launch_fast<MODE, XM, BT, 64, 5, RPS>(p, s); return true;
-            case 8: launch_fast<MODE, XM, BT, 64, 8, RPS>(p, s); return true;
+            case 3: return launch_fast<MODE, XM, BT, 64, 3, RPS>(p, s);
+            case 5: return launch_fast<MODE, XM, BT, 64, 5, RPS>(p, s);
+            case 8: return launch_fast<MODE, XM, BT, 64, 8, RPS>(p, s);
         }
     }
-    return false;
+    return 0;
 }
 
 template <int MODE, int XM, int BT>
-bool dispatch_rps(const Plan& pl, const GemvParams& p, hipStream_t s) {
+int dispatch_rps(const Plan& pl, const GemvParams& p, hipStream_t s) {
     if (pl.rps == 2) {
         if constexpr (MODE == kSwiglu) return dispatch_chunks<MODE, XM, BT, 2>(pl, p, s);
-        return false;
+        return 0;
     }
     return dispatch_chunks<MODE, XM, BT, 1>(pl, p, s);
 }
 
 template <int MODE, int XM>
-bool dispatch_fast(const Plan& pl, const GemvParams& p, hipStream_t s) {
+int dispatch_fast(const Plan& pl, const GemvParams& p, hipStream_t s) {  // grid size, 0 if none
     switch (pl.bt) {
         case 512: return dispatch_rps<MODE, XM, 512>(pl, p, s);
         case 1024: return dispatch_rps<MODE, XM, 1024>(pl, p, s);
@@ -778,4 +816,74 @@ extern "C" int qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(const uint16_t* 
     p.n_rows = 2 * intermediate_size;
     p.K = hidden_size;
     return launch_gemv<kSwiglu, kXRMS>(p, aligned(gate_up_qweight, 16) && act_fast_ok(p), stream, what);
+}
+
+// ---- fused LM head + sampling ------------------------------------------------------
+namespace qe {
+int launch_sample_stage2(const float* val, const int32_t* idx, int nparts, qe_device_control_block* d_control,
+                         int32_t* d_pinned, hipStream_t stream);
+namespace {
+template <int XM>
+int launch_lm_head_sample(GemvParams& p, float* scratch_val, int32_t* scratch_idx, qe_device_control_block* d_control,
+                          int32_t* d_pinned, hipStream_t stream, const char* what) {
+    QE_REQUIRE(scratch_val && scratch_idx, "%s: sample scratch is NULL", what);
+    QE_REQUIRE(p.K <= kMaxFastK, "%s: in_features=%d exceeds %d", what, p.K, kMaxFastK);
+    QE_REQUIRE(aligned(p.qw[0], 16) && act_fast_ok(p), "%s: weights and activations must be 16-byte aligned", what);
+    if (p.n_rows <= 0) return fail(QE_ERR_INVALID_ARGUMENT, "%s: vocab_size=%d", what, p.n_rows);
+    p.s_val = scratch_val;
+    p.s_idx = scratch_idx;
+    p.ctl = d_control;
+    const Plan pl = plan_for(p.K, p.n_rows, kPlain, XM != kXQ8);
+    const int parts = dispatch_fast<kSample, XM>(pl, p, stream);
+    if (parts <= 0) return fail(QE_ERR_UNSUPPORTED, "%s: no kernel for K=%d", what, p.K);
+    if (parts > QE_LM_HEAD_SAMPLE_PARTS) return fail(QE_ERR_UNSUPPORTED, "%s: %d partials", what, parts);
+    launch_sample_stage2(scratch_val, scratch_idx, parts, d_control, d_pinned, stream);
+    return check_launch(what);
+}
+}  // namespace
+}  // namespace qe
+
+extern "C" int qe_launch_gemv_lm_head_sample_w4a8(const uint32_t* qweight, const uint16_t* scales,
+                                                  const int8_t* input_q8, const float* input_scale,
+                                                  const int32_t* input_sum8, uint16_t* logits_opt,
+                                                  float* sample_scratch_val, int32_t* sample_scratch_idx,
+                                                  qe_device_control_block* d_control, int32_t* d_mapped_pinned_token,
+                                                  int vocab_size, int in_features, hipStream_t stream) {
+    const char* what = "gemv_lm_head_sample_w4a8";
+    if (int rc = check_k(what, in_features)) return rc;
+    QE_REQUIRE(input_q8 && input_scale && input_sum8 && qweight && scales, "%s: NULL pointer", what);
+    GemvParams p{};
+    p.qw[0] = qweight;
+    p.sc[0] = scales;
+    p.out[0] = logits_opt;
+    p.q8 = input_q8;
+    p.xs = input_scale;
+    p.s8 = input_sum8;
+    p.n_rows = vocab_size;
+    p.K = in_features;
+    return launch_lm_head_sample<kXQ8>(p, sample_scratch_val, sample_scratch_idx, d_control, d_mapped_pinned_token,
+                                       stream, what);
+}
+
+extern "C" int qe_launch_rmsnorm_gemv_lm_head_sample_w4a16(const uint16_t* input, const uint16_t* gamma,
+                                                           uint16_t* output_fp16_opt, const uint32_t* qweight,
+                                                           const uint16_t* scales, uint16_t* logits_opt,
+                                                           float* sample_scratch_val, int32_t* sample_scratch_idx,
+                                                           qe_device_control_block* d_control,
+                                                           int32_t* d_mapped_pinned_token, int vocab_size,
+                                                           int hidden_size, hipStream_t stream) {
+    const char* what = "rmsnorm_gemv_lm_head_sample_w4a16";
+    if (int rc = check_k(what, hidden_size)) return rc;
+    QE_REQUIRE(input && gamma && qweight && scales, "%s: NULL pointer", what);
+    GemvParams p{};
+    p.qw[0] = qweight;
+    p.sc[0] = scales;
+    p.out[0] = logits_opt;
+    p.x16 = input;
+    p.gamma = gamma;
+    p.norm_out = output_fp16_opt;
+    p.n_rows = vocab_size;
+    p.K = hidden_size;
+    return launch_lm_head_sample<kXRMS>(p, sample_scratch_val, sample_scratch_idx, d_control, d_mapped_pinned_token,
+                                        stream, what);
 }

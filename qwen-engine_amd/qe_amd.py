@@ -35,6 +35,8 @@ SIGNATURES = {
     "qe_launch_gemm_prefill_qkv_w4a16": [_P, _P, _I, _P, _I, _I, _I, _I, _I],
     "qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _I, _P, _I, _I],
     "qe_launch_sample_and_advance": [_P, _P, _P, _P, _P, _P, _I],
+    "qe_launch_gemv_lm_head_sample_w4a8": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P],
+    "qe_launch_rmsnorm_gemv_lm_head_sample_w4a16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P],
     "qe_launch_rmsnorm_gemv_qkv_w4a16": [_P, _P, _P, _P, _P, _I, _I, _I, _I],
     "qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _P, _P, _I, _I, _P],
     "qe_launch_embed_lookup_w4a16": [_P, _P, _P, _P, _P, _I, _P, _I],
@@ -209,7 +211,27 @@ def launch_sample_and_advance(logits, sample_scratch_val, sample_scratch_idx, d_
           _ptr(d_control), _ptr(d_mapped_pinned_token), _stream(stream), vocab_size)
 
 
+LM_HEAD_SAMPLE_PARTS = 2048  # QE_LM_HEAD_SAMPLE_PARTS
+
+
 # ---- fused decode entry points (no counterpart in the reference API) ---------
+def launch_gemv_lm_head_sample_w4a8(qweight, scales, input_q8, input_scale, input_sum8, logits_opt,
+                                    sample_scratch_val, sample_scratch_idx, d_control, d_mapped_pinned_token,
+                                    vocab_size=151936, in_features=1536, stream=None):
+    _call("qe_launch_gemv_lm_head_sample_w4a8", _ptr(qweight), _ptr(scales), _ptr(input_q8), _ptr(input_scale),
+          _ptr(input_sum8), _ptr(logits_opt), _ptr(sample_scratch_val), _ptr(sample_scratch_idx), _ptr(d_control),
+          _ptr(d_mapped_pinned_token), vocab_size, in_features, _stream(stream))
+
+
+def launch_rmsnorm_gemv_lm_head_sample_w4a16(input, gamma, output_fp16_opt, qweight, scales, logits_opt,
+                                             sample_scratch_val, sample_scratch_idx, d_control,
+                                             d_mapped_pinned_token, vocab_size=151936, hidden_size=1536,
+                                             stream=None):
+    _call("qe_launch_rmsnorm_gemv_lm_head_sample_w4a16", _ptr(input), _ptr(gamma), _ptr(output_fp16_opt),
+          _ptr(qweight), _ptr(scales), _ptr(logits_opt), _ptr(sample_scratch_val), _ptr(sample_scratch_idx),
+          _ptr(d_control), _ptr(d_mapped_pinned_token), vocab_size, hidden_size, _stream(stream))
+
+
 def launch_rmsnorm_gemv_qkv_w4a16(input, gamma, output_fp16_opt, view: QKVView, stream=None, hidden_size=1536,
                                   num_q_heads=12, num_kv_heads=2, head_dim=128):
     _call("qe_launch_rmsnorm_gemv_qkv_w4a16", _ptr(input), _ptr(gamma), _ptr(output_fp16_opt),

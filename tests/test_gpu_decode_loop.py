@@ -175,7 +175,7 @@ def _small_cfg(qe, fused=1):
     return c
 
 
-def test_engine_graph_matches_eager_and_is_deterministic(qe):
+def test_engine_graph_matches_eager_and_is_deterministic(qe, orc):
     prompt = [(i % 1000) + 100 for i in range(40)]  # the reference bench's synthetic prompt (cli_bench.cpp:78-82)
     e = qe.Engine(_small_cfg(qe), seed=7)
     t0 = e.prefill(prompt)
@@ -189,6 +189,7 @@ def test_engine_graph_matches_eager_and_is_deterministic(qe):
     assert e2.prefill(prompt) == t0 and e2.decode(12) == g
     assert all(0 <= t < 4096 for t in g)
     assert np.isfinite(e2.logits().astype(np.float32)).all()
+    assert g[-1] == orc.argmax_f16(e2.logits())  # fused LM head + sampling: token = argmax of its logits
     assert np.isfinite(e2.hidden_row0().astype(np.float32)).all()
     # the reference launch sequence computes the same integer stages: tokens agree
     e3 = qe.Engine(_small_cfg(qe, fused=0), seed=7)

@@ -301,3 +301,53 @@ def test_synth_distributions(orc):
     assert s.min() >= 0 and abs(s.mean() - 0.02 * np.sqrt(2 / np.pi)) < 1e-3
     x = orc.synth_f16_normal(5, 200000).astype(np.float64)
     assert abs(x.mean()) < 0.01 and abs(x.std() - 1) < 0.01
+
+
+# --------------------------------------------------------- sampling -------
+def test_philox4x32_10_known_answers(orc):
+    """Philox-4x32-10 known-answer vectors of the Random123 distribution
+    (Salmon et al., SC'11): counter, key -> output."""
+    kat = [
+        ([0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]),
+        ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]),
+        ([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0],
+         [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]),
+    ]
+    for ctr, key, want in kat:
+        assert list(orc.philox4x32_10(ctr, key)) == want
+
+
+def test_philox_uniform_placement_and_range(orc):
+    """sampling.cu:13-53: counter (subsequence, offset, 0, 0), key (seed lo,
+    seed hi), u = clamp((float(w0) + 1) / 4294967298.0f, 1e-7, 1 - 1e-7)."""
+    w0 = orc.philox4x32_10([0, 0, 0, 0], [0, 0])[0]
+    want = np.float32((np.float32(w0) + np.float32(1.0)) / np.float32(4294967298.0))
+    assert np.float32(orc.philox_uniform(0, 0, 0)) == want
+    seed = 0x299F31D0A4093822
+    w0 = orc.philox4x32_10([7, 11, 0, 0], [seed & 0xFFFFFFFF, seed >> 32])[0]
+    want = np.float32((np.float32(w0) + np.float32(1.0)) / np.float32(4294967298.0))
+    assert np.float32(orc.philox_uniform(seed, 7, 11)) == want
+    us = np.array([orc.philox_uniform(1234, i, 5) for i in range(20000)], np.float64)
+    assert us.min() >= np.float32(1e-7) and us.max() <= np.float32(1 - 1e-7)
+    hist = np.histogram(us, bins=20, range=(0, 1))[0]
+    chi2 = ((hist - 1000.0) ** 2 / 1000.0).sum()
+    assert chi2 < 50  # 19 dof: p ~ 1e-4 at 43
+
+
+def test_gumbel_sampling_follows_softmax(orc):
+    """Gumbel-max: argmax(l/T - log(-log u)) is distributed as softmax(l/T).
+    A sign or scale slip in the noise or temperature breaks the frequencies."""
+    logits = np.array([1.0, 0.0, -1.0, 0.5], np.float16)
+    T = 0.7
+    counts = np.zeros(4)
+    n = 6000
+    for pos in range(n):
+        tok, _ = orc.sample_f16(logits, T, 42, pos)
+        counts[tok] += 1
+    p = np.exp(logits.astype(np.float64) / T)
+    p /= p.sum()
+    chi2 = ((counts - n * p) ** 2 / (n * p)).sum()
+    assert chi2 < 20  # 3 dof
+    # temperature <= 1e-5 is greedy
+    tok, vals = orc.sample_f16(logits, 1e-6, 42, 3)
+    assert tok == 0 and np.array_equal(vals, logits.astype(np.float32))
