@@ -311,7 +311,19 @@ def main():
         qe_amd.launch_sample_and_advance(logits, val, idx, None, tok, vocab_size=V)
 
     ms = time_graph(graph_of(lm_argmax, C), 5) / C
-    result["lm_head_argmax"] = {"us": round(ms * 1e3, 3), "GB/s": round(gemv_bytes(V, H) / (ms * 1e-3) / 1e9, 1)}
+    result["lm_head_argmax"] = {"us": round(ms * 1e3, 3), "GB/s": round(gemv_bytes(V, H) / (ms * 1e-3) / 1e9, 1),
+                                "launches": 3}
+    # fused: LM-head GEMV with the first sampling stage in its epilogue + stage 2 (2 launches, no logits)
+    fval = torch.empty(qe_amd.LM_HEAD_SAMPLE_PARTS, dtype=torch.float32, device=dev)
+    fidx = torch.empty(qe_amd.LM_HEAD_SAMPLE_PARTS, dtype=torch.int32, device=dev)
+
+    def lm_fused(i):
+        qe_amd.launch_gemv_lm_head_sample_w4a8(wl[i % C], sl[i % C], q8, xs, s8, None, fval, fidx, None, tok,
+                                               vocab_size=V, in_features=H)
+
+    ms = time_graph(graph_of(lm_fused, C), 5) / C
+    result["lm_head_sample_fused"] = {"us": round(ms * 1e3, 3),
+                                      "GB/s": round(gemv_bytes(V, H) / (ms * 1e-3) / 1e9, 1), "launches": 2}
     del wl, sl
 
     # ---------------- prefill dequant-GEMM -----------------------
