@@ -1,14 +1,15 @@
 /*
  * qe_engine.h — C-ABI of the minimal Qwen2.5-style decode engine built on the
- * W4A16 G128 path.  Weights are random-initialized on the device in the
- * packed .qwenbin layout (uint32 [N][K/8] nibbles, fp16 [N][K/128] scales);
- * the LM head is tied to the embedding.  One engine = one HIP stream, one
- * device arena (allocated at create), one captured decode graph.
+ * W4A16 G128 path.  Weights are either random-initialized on the device in
+ * the packed .qwenbin layout (uint32 [N][K/8] nibbles, fp16 [N][K/128]
+ * scales, LM head tied to the embedding) or loaded from a .qwenbin v2 file
+ * (include/qwenbin.h).  One engine = one HIP stream, one device arena
+ * (allocated at create), one captured decode graph.
  *
  * Counterpart of the reference's QwenEngine (include/engine.cuh:104-226):
- * prefill (:prefill), decode_step (:decode_step) and profile_stages.
- * Session leasing, rollback, prefix reuse and the .qwenbin loader are not
- * part of this build.
+ * construction from a .qwenbin (load_model_file + setup_arena), prefill
+ * (:prefill), decode_step (:decode_step) and profile_stages.  Session
+ * leasing, rollback and prefix reuse are not part of this build.
  */
 #ifndef QE_ENGINE_H
 #define QE_ENGINE_H
@@ -42,6 +43,22 @@ void qe_engine_default_config(qe_engine_config* cfg);
 int qe_engine_create(const qe_engine_config* cfg, uint64_t seed, qe_engine** out);
 void qe_engine_destroy(qe_engine* e);
 
+/* Build an engine from a .qwenbin v2 file (QwenEngine::QwenEngine ->
+ * load_model_file + setup_arena, src/engine.cu:85-348): the file is validated
+ * as qe_qwenbin_inspect does, its payload [weights_offset, end) is copied to
+ * the device once and every tensor is addressed by its offset; an untied
+ * lm_head is used when present.  max_seq_len: 0 takes the file's (4096 when
+ * the file's is 0 or above 32768), otherwise capped by the file's.
+ * prefill_chunk 0 means 1024.  The reference also requires the exact
+ * Qwen2.5-1.5B dimensions; this build accepts any the kernels support. */
+int qe_engine_create_from_qwenbin(const char* path, int max_seq_len, int prefill_chunk, int fused_decode,
+                                  qe_engine** out);
+
+/* Write the engine's weights as a .qwenbin v2 file in the layout of the
+ * reference's exporter (tools/export_qwen25.py:218-419): 4096-byte header,
+ * layer table at 4096, 256-byte aligned tensors. */
+int qe_engine_save_qwenbin(qe_engine* e, const char* path);
+
 /* Position 0, token 0 (the KV cache is overwritten as positions advance). */
 int qe_engine_reset(qe_engine* e);
 
@@ -73,7 +90,9 @@ int qe_engine_read_hidden(qe_engine* e, uint16_t* host, int n);
 
 /* Synchronize and copy the first `bytes` of a named engine buffer to host
  * memory: "logits", "hidden", "q8", "q8_scale", "q8_sum8", "embed_w",
- * "embed_s", "final_norm", "control". */
+ * "embed_s", "lm_head_w", "lm_head_s", "final_norm", "control", or a layer
+ * tensor "layer<l>.<t>" with t one of ln1 ln2 q_w q_s k_w k_s v_w v_s o_w o_s
+ * gate_up_w gate_up_s down_w down_s q_bias k_bias v_bias. */
 int qe_engine_read_buffer(qe_engine* e, const char* name, void* host, size_t bytes);
 
 #ifdef __cplusplus

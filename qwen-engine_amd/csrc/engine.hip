@@ -1,5 +1,7 @@
 // Minimal decode engine over the W4A16 G128 path (gfx950): random-init
-// Qwen2.5-style weights in the packed layout, chunked prefill on the MFMA
+// Qwen2.5-style weights in the packed layout or a .qwenbin v2 file (loaded as
+// the reference's setup_arena does: one device copy of the payload, tensors
+// addressed by offset), chunked prefill on the MFMA
 // dequant-GEMMs, and a decode step captured once into a HIP graph that is
 // replayed per token, driven by a device control block (token id, position)
 // so the graph needs no parameter updates.
@@ -20,6 +22,7 @@
 
 #include "qe_common.hpp"
 #include "qe_engine.h"
+#include "qwenbin_internal.hpp"
 
 namespace qe {
 namespace {
@@ -79,7 +82,9 @@ struct qe_engine {
     char* arena = nullptr;
     size_t arena_size = 0, arena_used = 0;
     std::vector<qe::Layer> layers;
-    qe::Mat embed;  // tied LM head
+    qe::Mat embed;
+    qe::Mat lm;           // LM head: the embedding when tied
+    void* payload = nullptr;  // weights loaded from a .qwenbin (one device copy of the file's payload)
     uint16_t* final_norm = nullptr;
     // workspace
     uint16_t *act0 = nullptr, *act1 = nullptr, *dq = nullptr, *dk = nullptr, *dv = nullptr, *attn = nullptr,
@@ -219,7 +224,7 @@ int decode_pass(qe_engine* e, Timer* t) {
         QE_TRY(mark(e, t, 0));
     }
     if (c.fused_decode) {  // final RMSNorm + tied LM head + sampling stage 1, then stage 2 + advance
-        QE_TRY(qe_launch_rmsnorm_gemv_lm_head_sample_w4a16(e->act0, e->final_norm, nullptr, e->embed.w, e->embed.s,
+        QE_TRY(qe_launch_rmsnorm_gemv_lm_head_sample_w4a16(e->act0, e->final_norm, nullptr, e->lm.w, e->lm.s,
                                                            e->logits, e->sample_val, e->sample_idx, e->ctl,
                                                            e->d_token, c.vocab_size, H, s));
         QE_TRY(mark(e, t, 0));
@@ -227,7 +232,7 @@ int decode_pass(qe_engine* e, Timer* t) {
     }
     QE_TRY(qe_launch_rmsnorm_q8_1(e->act0, e->final_norm, nullptr, e->q8, e->q8_scale, e->q8_sum8, s, H));
     QE_TRY(mark(e, t, 2));
-    QE_TRY(qe_launch_gemv_w4a8(e->embed.w, e->embed.s, e->q8, e->q8_scale, e->q8_sum8, nullptr, e->logits,
+    QE_TRY(qe_launch_gemv_w4a8(e->lm.w, e->lm.s, e->q8, e->q8_scale, e->q8_sum8, nullptr, e->logits,
                                c.vocab_size, H, s));
     QE_TRY(mark(e, t, 0));
     QE_TRY(qe_launch_sample_and_advance(e->logits, e->sample_val, e->sample_idx, e->ctl, e->d_token, s,
@@ -307,60 +312,63 @@ extern "C" void qe_engine_destroy(qe_engine* e) {
     if (e->graph) (void)hipGraphDestroy(e->graph);
     if (e->h_token) (void)hipHostFree(e->h_token);
     if (e->arena) (void)hipFree(e->arena);
+    if (e->payload) (void)hipFree(e->payload);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     delete e;
 }
 
-extern "C" int qe_engine_create(const qe_engine_config* cfg, uint64_t seed, qe_engine** out) {
-    QE_REQUIRE(cfg && out, "engine_create: NULL argument");
-    *out = nullptr;
-    const qe_engine_config& c = *cfg;
-    QE_REQUIRE(c.num_layers > 0 && c.hidden_size % 128 == 0 && c.intermediate_size % 128 == 0 && c.head_dim == 128 &&
-                   c.num_kv_heads > 0 && c.num_q_heads % c.num_kv_heads == 0 && c.vocab_size > 0 &&
-                   c.max_seq_len > 0 && c.prefill_chunk > 0 && c.num_q_heads * c.head_dim == c.hidden_size,
-               "engine_create: unsupported configuration");
-    std::unique_ptr<qe_engine, void (*)(qe_engine*)> e(new qe_engine(), qe_engine_destroy);
-    e->cfg = c;
+namespace qe {
+namespace {
+
+bool config_ok(const qe_engine_config& c) {
+    return c.num_layers > 0 && c.hidden_size > 0 && c.hidden_size % 128 == 0 && c.intermediate_size > 0 &&
+           c.intermediate_size % 128 == 0 && c.head_dim == 128 && c.num_kv_heads > 0 &&
+           c.num_q_heads % c.num_kv_heads == 0 && c.vocab_size > 0 && c.max_seq_len > 0 && c.prefill_chunk > 0 &&
+           c.num_q_heads * c.head_dim == c.hidden_size;
+}
+
+size_t weight_bytes(const qe_engine_config& c) {
     const int H = c.hidden_size, I = c.intermediate_size, qd = c.num_q_heads * c.head_dim,
-              kvd = c.num_kv_heads * c.head_dim, T = c.prefill_chunk;
-    size_t bytes = 0;
+              kvd = c.num_kv_heads * c.head_dim;
     const size_t per_layer = mat_bytes(qd, H) + 2 * mat_bytes(kvd, H) + mat_bytes(H, qd) + mat_bytes(2 * I, H) +
                              mat_bytes(H, I) + align256(H * 2) * 2 + align256(qd * 2) + align256(kvd * 2) * 2;
-    bytes += per_layer * c.num_layers + mat_bytes(c.vocab_size, H) + align256(H * 2);
-    bytes += 2 * align256(static_cast<size_t>(c.num_layers) * c.num_kv_heads * c.max_seq_len * c.head_dim * 2);
+    return per_layer * c.num_layers + mat_bytes(c.vocab_size, H) + align256(H * 2);
+}
+
+// Q8_1 scratch holds the longest quantized activation: the down input (I),
+// the normalized hidden state (H) or the attention output (q_dim)
+int q8_len(const qe_engine_config& c) {
+    return std::max(c.intermediate_size, std::max(c.hidden_size, c.num_q_heads * c.head_dim));
+}
+
+size_t workspace_bytes(const qe_engine_config& c) {
+    const int H = c.hidden_size, I = c.intermediate_size, qd = c.num_q_heads * c.head_dim,
+              kvd = c.num_kv_heads * c.head_dim, T = c.prefill_chunk, QN = q8_len(c);
+    size_t bytes = 2 * align256(static_cast<size_t>(c.num_layers) * c.num_kv_heads * c.max_seq_len * c.head_dim * 2);
     bytes += 2 * align256(static_cast<size_t>(T) * H * 2) + align256(static_cast<size_t>(T) * qd * 2) +
              2 * align256(static_cast<size_t>(T) * kvd * 2) + align256(static_cast<size_t>(T) * qd * 2) +
              align256(static_cast<size_t>(T) * I * 2) + align256(static_cast<size_t>(c.vocab_size) * 2);
-    // Q8_1 scratch holds the longest quantized activation: the down input (I),
-    // the normalized hidden state (H) or the attention output (q_dim)
-    const int QN = std::max(I, std::max(H, qd));
     bytes += align256(QN) + align256(QN / 128 * 4) + align256(QN / 8 * 4);
-    bytes += 2 * align256(static_cast<size_t>(c.num_q_heads) * 16 * 128 * 4) + 2 * align256(256 * 4) +
-             align256(static_cast<size_t>(c.max_seq_len) * 4) + 256 + 256 + 4096;
+    bytes += 2 * align256(static_cast<size_t>(c.num_q_heads) * 16 * 128 * 4) +
+             2 * align256(QE_LM_HEAD_SAMPLE_PARTS * 4) + align256(static_cast<size_t>(c.max_seq_len) * 4) + 256 +
+             256 + 4096;
+    return bytes;
+}
+
+int begin_engine(qe_engine* e, const qe_engine_config& c, size_t arena_bytes) {
+    e->cfg = c;
     QE_HIP(hipStreamCreate(&e->stream));
-    QE_HIP(hipMalloc(&e->arena, bytes));
-    e->arena_size = bytes;
+    QE_HIP(hipMalloc(&e->arena, arena_bytes));
+    e->arena_size = arena_bytes;
     QE_HIP(hipHostMalloc(reinterpret_cast<void**>(&e->h_token), sizeof(int32_t), hipHostMallocMapped));
     QE_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&e->d_token), e->h_token, 0));
+    return QE_OK;
+}
 
-    // layout first, then check, then initialize
-    e->layers.resize(c.num_layers);
-    for (int l = 0; l < c.num_layers; ++l) {
-        Layer& L = e->layers[l];
-        L.q = alloc_mat(e.get(), qd, H);
-        L.k = alloc_mat(e.get(), kvd, H);
-        L.v = alloc_mat(e.get(), kvd, H);
-        L.o = alloc_mat(e.get(), H, qd);
-        L.gate_up = alloc_mat(e.get(), 2 * I, H);
-        L.down = alloc_mat(e.get(), H, I);
-        L.ln1 = e->take<uint16_t>(H * 2);
-        L.ln2 = e->take<uint16_t>(H * 2);
-        L.q_bias = e->take<uint16_t>(qd * 2);
-        L.k_bias = e->take<uint16_t>(kvd * 2);
-        L.v_bias = e->take<uint16_t>(kvd * 2);
-    }
-    e->embed = alloc_mat(e.get(), c.vocab_size, H);
-    e->final_norm = e->take<uint16_t>(H * 2);
+void layout_workspace(qe_engine* e) {
+    const qe_engine_config& c = e->cfg;
+    const int H = c.hidden_size, I = c.intermediate_size, qd = c.num_q_heads * c.head_dim,
+              kvd = c.num_kv_heads * c.head_dim, T = c.prefill_chunk, QN = q8_len(c);
     const size_t kvb = static_cast<size_t>(c.num_layers) * e->kv_stride() * 2;
     e->kcache = e->take<uint16_t>(kvb);
     e->vcache = e->take<uint16_t>(kvb);
@@ -381,6 +389,54 @@ extern "C" int qe_engine_create(const qe_engine_config* cfg, uint64_t seed, qe_e
     e->sample_idx = e->take<int32_t>(QE_LM_HEAD_SAMPLE_PARTS * 4);
     e->tokens = e->take<int32_t>(static_cast<size_t>(c.max_seq_len) * 4);
     e->ctl = e->take<qe_device_control_block>(sizeof(qe_device_control_block));
+}
+
+// KV cache cleared, control block at position 0, decode graph captured
+int finish_engine(qe_engine* e) {
+    QE_REQUIRE(e->arena_used <= e->arena_size, "engine_create: arena overflow (%zu > %zu)", e->arena_used,
+               e->arena_size);
+    (void)cu_count();  // cache the device fact before graph capture
+    const size_t kvb = static_cast<size_t>(e->cfg.num_layers) * e->kv_stride() * 2;
+    QE_HIP(hipMemsetAsync(e->kcache, 0, kvb, e->stream));
+    QE_HIP(hipMemsetAsync(e->vcache, 0, kvb, e->stream));
+    const qe_device_control_block init = {0, 0, 0.0f, 0, 1337ull};
+    QE_HIP(hipMemcpyAsync(e->ctl, &init, sizeof(init), hipMemcpyHostToDevice, e->stream));
+    QE_HIP(hipStreamSynchronize(e->stream));
+    return capture_graph(e);
+}
+
+}  // namespace
+}  // namespace qe
+
+extern "C" int qe_engine_create(const qe_engine_config* cfg, uint64_t seed, qe_engine** out) {
+    QE_REQUIRE(cfg && out, "engine_create: NULL argument");
+    *out = nullptr;
+    const qe_engine_config& c = *cfg;
+    QE_REQUIRE(config_ok(c), "engine_create: unsupported configuration");
+    std::unique_ptr<qe_engine, void (*)(qe_engine*)> e(new qe_engine(), qe_engine_destroy);
+    QE_TRY(begin_engine(e.get(), c, weight_bytes(c) + workspace_bytes(c)));
+    const int H = c.hidden_size, I = c.intermediate_size, qd = c.num_q_heads * c.head_dim,
+              kvd = c.num_kv_heads * c.head_dim;
+    // layout first, then check, then initialize
+    e->layers.resize(c.num_layers);
+    for (int l = 0; l < c.num_layers; ++l) {
+        Layer& L = e->layers[l];
+        L.q = alloc_mat(e.get(), qd, H);
+        L.k = alloc_mat(e.get(), kvd, H);
+        L.v = alloc_mat(e.get(), kvd, H);
+        L.o = alloc_mat(e.get(), H, qd);
+        L.gate_up = alloc_mat(e.get(), 2 * I, H);
+        L.down = alloc_mat(e.get(), H, I);
+        L.ln1 = e->take<uint16_t>(H * 2);
+        L.ln2 = e->take<uint16_t>(H * 2);
+        L.q_bias = e->take<uint16_t>(qd * 2);
+        L.k_bias = e->take<uint16_t>(kvd * 2);
+        L.v_bias = e->take<uint16_t>(kvd * 2);
+    }
+    e->embed = alloc_mat(e.get(), c.vocab_size, H);
+    e->lm = e->embed;
+    e->final_norm = e->take<uint16_t>(H * 2);
+    layout_workspace(e.get());
     QE_REQUIRE(e->arena_used <= e->arena_size, "engine_create: arena overflow (%zu > %zu)", e->arena_used,
                e->arena_size);
     uint64_t sd = seed * 0x100000001B3ull + 17;
@@ -395,16 +451,150 @@ extern "C" int qe_engine_create(const qe_engine_config* cfg, uint64_t seed, qe_e
     }
     QE_TRY(init_mat(e.get(), e->embed, sd++, false));
     QE_TRY(init_vec(e.get(), e->final_norm, H, sd++, 1.0f, 0.0f));
-    (void)cu_count();  // cache the device fact before graph capture
-    QE_HIP(hipMemsetAsync(e->kcache, 0, kvb, e->stream));
-    QE_HIP(hipMemsetAsync(e->vcache, 0, kvb, e->stream));
-    const qe_device_control_block init = {0, 0, 0.0f, 0, 1337ull};
-    QE_HIP(hipMemcpyAsync(e->ctl, &init, sizeof(init), hipMemcpyHostToDevice, e->stream));
-    QE_HIP(hipStreamSynchronize(e->stream));
-    QE_TRY(capture_graph(e.get()));
+    QE_TRY(finish_engine(e.get()));
     *out = e.release();
     clear_error();
     return QE_OK;
+}
+
+extern "C" int qe_engine_create_from_qwenbin(const char* path, int max_seq_len, int prefill_chunk, int fused_decode,
+                                             qe_engine** out) {
+    QE_REQUIRE(path && out, "engine_create_from_qwenbin: NULL argument");
+    *out = nullptr;
+    MappedFile file;
+    QE_TRY(file.open(path));
+    QwenbinModel m;
+    QE_TRY(qwenbin_parse(file, m));
+    const qe_qwenbin_info& in = m.info;
+    qe_engine_config c{};
+    c.num_layers = in.num_layers;
+    c.hidden_size = in.hidden_size;
+    c.intermediate_size = in.intermediate_size;
+    c.num_q_heads = in.num_q_heads;
+    c.num_kv_heads = in.num_kv_heads;
+    c.head_dim = in.head_dim;
+    c.vocab_size = in.vocab_size;
+    c.rope_theta = in.rope_theta;
+    // context window: the caller's, capped by the file's; the file's when 0
+    // (src/engine.cu:128-132 caps the same way); 4096 when neither is usable
+    const int file_seq = (in.max_seq_len > 0 && in.max_seq_len <= 32768) ? in.max_seq_len : 4096;
+    c.max_seq_len = max_seq_len > 0 ? std::min(max_seq_len, file_seq) : file_seq;
+    c.prefill_chunk = prefill_chunk > 0 ? prefill_chunk : 1024;
+    c.fused_decode = fused_decode;
+    QE_REQUIRE(config_ok(c), "engine_create_from_qwenbin: unsupported configuration");
+    std::unique_ptr<qe_engine, void (*)(qe_engine*)> e(new qe_engine(), qe_engine_destroy);
+    QE_TRY(begin_engine(e.get(), c, workspace_bytes(c)));
+    // one device copy of the payload [weights_offset, end of file) (src/engine.cu:271-272)
+    QE_HIP(hipMalloc(&e->payload, std::max<uint64_t>(in.weights_bytes, 256)));
+    QE_HIP(hipMemcpy(e->payload, file.data() + in.weights_offset, in.weights_bytes, hipMemcpyHostToDevice));
+    char* base = static_cast<char*>(e->payload);
+    auto at = [&](uint64_t off) -> char* { return off == 0 ? nullptr : base + (off - in.weights_offset); };
+    auto mat = [&](uint64_t w, uint64_t sc, int rows, int K) {
+        Mat x;
+        x.w = reinterpret_cast<uint32_t*>(at(w));
+        x.s = reinterpret_cast<uint16_t*>(at(sc));
+        x.rows = rows;
+        x.K = K;
+        return x;
+    };
+    const int H = c.hidden_size, I = c.intermediate_size, qd = c.num_q_heads * c.head_dim,
+              kvd = c.num_kv_heads * c.head_dim;
+    const qe_qwenbin_header& h = m.header;
+    e->embed = mat(h.embed_tokens_offset, h.reserved[0], c.vocab_size, H);
+    e->lm = m.untied_lm_head ? mat(h.lm_head_offset, h.reserved[1], c.vocab_size, H) : e->embed;
+    e->final_norm = reinterpret_cast<uint16_t*>(at(h.final_norm_offset));
+    e->layers.resize(c.num_layers);
+    for (int l = 0; l < c.num_layers; ++l) {
+        const qe_qwenbin_layer& d = m.layers[l];
+        Layer& L = e->layers[l];
+        L.ln1 = reinterpret_cast<uint16_t*>(at(d.norm1_weight_offset));
+        L.ln2 = reinterpret_cast<uint16_t*>(at(d.norm2_weight_offset));
+        L.q_bias = reinterpret_cast<uint16_t*>(at(d.q_bias_offset));
+        L.k_bias = reinterpret_cast<uint16_t*>(at(d.k_bias_offset));
+        L.v_bias = reinterpret_cast<uint16_t*>(at(d.v_bias_offset));
+        L.q = mat(d.qkv_weight_offset, d.q_scale_offset, qd, H);
+        L.k = mat(d.k_weight_offset, d.k_scale_offset, kvd, H);
+        L.v = mat(d.v_weight_offset, d.v_scale_offset, kvd, H);
+        L.o = mat(d.attn_out_weight_offset, d.attn_out_scale_offset, H, qd);
+        L.gate_up = mat(d.mlp_gate_offset, d.mlp_gate_scale_offset, 2 * I, H);
+        L.down = mat(d.mlp_down_offset, d.mlp_down_scale_offset, H, I);
+    }
+    layout_workspace(e.get());
+    QE_TRY(finish_engine(e.get()));
+    *out = e.release();
+    clear_error();
+    return QE_OK;
+}
+
+extern "C" int qe_engine_save_qwenbin(qe_engine* e, const char* path) {
+    QE_REQUIRE(e && path, "engine_save_qwenbin: NULL argument");
+    QE_HIP(hipStreamSynchronize(e->stream));
+    const qe_engine_config& c = e->cfg;
+    const int H = c.hidden_size, I = c.intermediate_size, qd = c.num_q_heads * c.head_dim,
+              kvd = c.num_kv_heads * c.head_dim;
+    QwenbinWriter wr(c.num_layers);
+    std::vector<uint8_t> host;
+    int rc = QE_OK;
+    // copy a device tensor into the container; 0 for an absent (NULL) tensor
+    auto put = [&](const void* dptr, size_t bytes) -> uint64_t {
+        if (dptr == nullptr || rc != QE_OK) return 0;
+        host.resize(bytes);
+        const hipError_t err = hipMemcpy(host.data(), dptr, bytes, hipMemcpyDeviceToHost);
+        if (err != hipSuccess) {
+            rc = fail(QE_ERR_HIP, "engine_save_qwenbin: %s", hipGetErrorString(err));
+            return 0;
+        }
+        return wr.add(host.data(), bytes);
+    };
+    auto wbytes = [](const Mat& x) { return static_cast<size_t>(x.rows) * x.K / 2; };
+    auto sbytes = [](const Mat& x) { return static_cast<size_t>(x.rows) * (x.K / 128) * 2; };
+    qe_qwenbin_header& h = wr.header();
+    // the exporter's order (tools/export_qwen25.py:238-362)
+    h.embed_tokens_offset = put(e->embed.w, wbytes(e->embed));
+    h.reserved[0] = put(e->embed.s, sbytes(e->embed));
+    const bool tied = e->lm.w == e->embed.w;
+    if (tied) {
+        h.lm_head_offset = h.embed_tokens_offset;
+    } else {
+        h.lm_head_offset = put(e->lm.w, wbytes(e->lm));
+        h.reserved[1] = put(e->lm.s, sbytes(e->lm));
+    }
+    h.final_norm_offset = put(e->final_norm, static_cast<size_t>(H) * 2);
+    for (int l = 0; l < c.num_layers; ++l) {
+        const Layer& L = e->layers[l];
+        qe_qwenbin_layer& d = wr.layer(l);
+        d.type = QE_QWENBIN_LAYER_GQA;
+        d.norm1_weight_offset = put(L.ln1, static_cast<size_t>(H) * 2);
+        d.qkv_weight_offset = put(L.q.w, wbytes(L.q));
+        d.q_scale_offset = put(L.q.s, sbytes(L.q));
+        d.k_weight_offset = put(L.k.w, wbytes(L.k));
+        d.k_scale_offset = put(L.k.s, sbytes(L.k));
+        d.v_weight_offset = put(L.v.w, wbytes(L.v));
+        d.v_scale_offset = put(L.v.s, sbytes(L.v));
+        d.q_bias_offset = put(L.q_bias, static_cast<size_t>(qd) * 2);
+        d.k_bias_offset = put(L.k_bias, static_cast<size_t>(kvd) * 2);
+        d.v_bias_offset = put(L.v_bias, static_cast<size_t>(kvd) * 2);
+        d.attn_out_weight_offset = put(L.o.w, wbytes(L.o));
+        d.attn_out_scale_offset = put(L.o.s, sbytes(L.o));
+        d.norm2_weight_offset = put(L.ln2, static_cast<size_t>(H) * 2);
+        d.mlp_gate_offset = d.mlp_up_offset = put(L.gate_up.w, wbytes(L.gate_up));
+        d.mlp_gate_scale_offset = d.mlp_up_scale_offset = put(L.gate_up.s, sbytes(L.gate_up));
+        d.mlp_down_offset = put(L.down.w, wbytes(L.down));
+        d.mlp_down_scale_offset = put(L.down.s, sbytes(L.down));
+        d.quant_scales_offset = d.q_scale_offset;
+    }
+    if (rc != QE_OK) return rc;
+    h.hidden_size = static_cast<uint32_t>(H);
+    h.intermediate_size = static_cast<uint32_t>(I);
+    h.num_attention_heads = static_cast<uint32_t>(c.num_q_heads);
+    h.num_kv_heads = static_cast<uint32_t>(c.num_kv_heads);
+    h.head_dim = static_cast<uint32_t>(c.head_dim);
+    h.vocab_size = static_cast<uint32_t>(c.vocab_size);
+    h.max_seq_len = static_cast<uint32_t>(c.max_seq_len);
+    h.tie_word_embeddings = tied ? 1u : 0u;
+    h.rms_norm_eps = 1e-6f;
+    h.rope_theta = c.rope_theta;
+    return wr.write(path);
 }
 
 extern "C" int qe_engine_reset(qe_engine* e) {
@@ -435,7 +625,7 @@ extern "C" int qe_engine_prefill(qe_engine* e, const int32_t* tokens, int n, int
     const int last = (n - 1) % c.prefill_chunk;
     QE_TRY(qe_launch_rmsnorm_q8_1(e->act0 + static_cast<size_t>(last) * c.hidden_size, e->final_norm, nullptr, e->q8,
                                   e->q8_scale, e->q8_sum8, e->stream, c.hidden_size));
-    QE_TRY(qe_launch_gemv_w4a8(e->embed.w, e->embed.s, e->q8, e->q8_scale, e->q8_sum8, nullptr, e->logits,
+    QE_TRY(qe_launch_gemv_w4a8(e->lm.w, e->lm.s, e->q8, e->q8_scale, e->q8_sum8, nullptr, e->logits,
                                c.vocab_size, c.hidden_size, e->stream));
     QE_TRY(qe_launch_sample_and_advance(e->logits, e->sample_val, e->sample_idx, e->ctl, e->d_token, e->stream,
                                         c.vocab_size));
@@ -535,9 +725,41 @@ extern "C" int qe_engine_read_buffer(qe_engine* e, const char* name, void* host,
         {"q8_sum8", e->q8_sum8, static_cast<size_t>(qn / 8) * 4},
         {"embed_w", e->embed.w, static_cast<size_t>(c.vocab_size) * c.hidden_size / 2},
         {"embed_s", e->embed.s, static_cast<size_t>(c.vocab_size) * (c.hidden_size / 128) * 2},
+        {"lm_head_w", e->lm.w, static_cast<size_t>(c.vocab_size) * c.hidden_size / 2},
+        {"lm_head_s", e->lm.s, static_cast<size_t>(c.vocab_size) * (c.hidden_size / 128) * 2},
         {"final_norm", e->final_norm, static_cast<size_t>(c.hidden_size) * 2},
         {"control", e->ctl, sizeof(qe_device_control_block)},
     };
+    // "layer<l>.<tensor>" and the LM head
+    int l = -1;
+    char t[32] = {0};
+    if (std::sscanf(name, "layer%d.%31s", &l, t) == 2) {
+        QE_REQUIRE(l >= 0 && l < c.num_layers, "engine_read_buffer: layer %d outside [0, %d)", l, c.num_layers);
+        const Layer& L = e->layers[l];
+        const int H = c.hidden_size, qd = c.num_q_heads * c.head_dim, kvd = c.num_kv_heads * c.head_dim;
+        auto wb = [](const Mat& x) { return static_cast<size_t>(x.rows) * x.K / 2; };
+        auto sb = [](const Mat& x) { return static_cast<size_t>(x.rows) * (x.K / 128) * 2; };
+        const Item li[] = {
+            {"ln1", L.ln1, static_cast<size_t>(H) * 2}, {"ln2", L.ln2, static_cast<size_t>(H) * 2},
+            {"q_w", L.q.w, wb(L.q)}, {"q_s", L.q.s, sb(L.q)}, {"k_w", L.k.w, wb(L.k)}, {"k_s", L.k.s, sb(L.k)},
+            {"v_w", L.v.w, wb(L.v)}, {"v_s", L.v.s, sb(L.v)}, {"o_w", L.o.w, wb(L.o)}, {"o_s", L.o.s, sb(L.o)},
+            {"gate_up_w", L.gate_up.w, wb(L.gate_up)}, {"gate_up_s", L.gate_up.s, sb(L.gate_up)},
+            {"down_w", L.down.w, wb(L.down)}, {"down_s", L.down.s, sb(L.down)},
+            {"q_bias", L.q_bias, static_cast<size_t>(qd) * 2}, {"k_bias", L.k_bias, static_cast<size_t>(kvd) * 2},
+            {"v_bias", L.v_bias, static_cast<size_t>(kvd) * 2},
+        };
+        for (const Item& it : li) {
+            if (std::strcmp(it.n, t) == 0) {
+                QE_REQUIRE(it.p != nullptr, "engine_read_buffer: '%s' is absent", name);
+                QE_REQUIRE(bytes <= it.size, "engine_read_buffer: %zu bytes requested, '%s' holds %zu", bytes, name,
+                           it.size);
+                QE_HIP(hipStreamSynchronize(e->stream));
+                QE_HIP(hipMemcpy(host, it.p, bytes, hipMemcpyDeviceToHost));
+                return QE_OK;
+            }
+        }
+        return fail(QE_ERR_INVALID_ARGUMENT, "engine_read_buffer: unknown layer tensor '%s'", t);
+    }
     for (const Item& it : items) {
         if (std::strcmp(it.n, name) == 0) {
             QE_REQUIRE(bytes <= it.size, "engine_read_buffer: %zu bytes requested, '%s' holds %zu", bytes, name, it.size);

@@ -62,6 +62,9 @@ ENGINE_SIGNATURES = {
     "qe_engine_read_logits": [_P, _P, _I],
     "qe_engine_read_hidden": [_P, _P, _I],
     "qe_engine_read_buffer": [_P, ctypes.c_char_p, _P, ctypes.c_size_t],
+    "qe_engine_create_from_qwenbin": [ctypes.c_char_p, _I, _I, _I, _P],
+    "qe_engine_save_qwenbin": [_P, ctypes.c_char_p],
+    "qe_qwenbin_inspect": [ctypes.c_char_p, _P],
 }
 
 _lib = None
@@ -295,14 +298,57 @@ def default_config() -> EngineConfig:
     return c
 
 
-class Engine:
-    """Random-init Qwen2.5-style decode engine (include/qe_engine.h)."""
+class QwenbinInfo(ctypes.Structure):
+    """qe_qwenbin_info (include/qwenbin.h)."""
+    _fields_ = [("version", ctypes.c_uint32), ("quant_type", ctypes.c_uint32),
+                ("tie_word_embeddings", ctypes.c_uint32), ("hidden_size", _I), ("intermediate_size", _I),
+                ("num_layers", _I), ("num_q_heads", _I), ("num_kv_heads", _I), ("head_dim", _I),
+                ("vocab_size", _I), ("max_seq_len", _I), ("rms_norm_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float), ("file_size", ctypes.c_uint64), ("weights_offset", ctypes.c_uint64),
+                ("weights_bytes", ctypes.c_uint64)]
 
-    def __init__(self, cfg: EngineConfig | None = None, seed: int = 42):
+
+def qwenbin_inspect(path: str) -> dict:
+    """qe_qwenbin_inspect: validate a .qwenbin v2 file (no GPU); raises RuntimeError on a bad file."""
+    info = QwenbinInfo()
+    _check(lib().qe_qwenbin_inspect(str(path).encode(), ctypes.byref(info)), "qe_qwenbin_inspect")
+    return {n: getattr(info, n) for n, _ in QwenbinInfo._fields_}
+
+
+class Engine:
+    """Qwen2.5-style decode engine (include/qe_engine.h): random-init, or
+    Engine.from_qwenbin(path) for a .qwenbin v2 file."""
+
+    def __init__(self, cfg: EngineConfig | None = None, seed: int = 42, _handle=None):
+        if _handle is not None:
+            self._h = _handle
+            self.cfg = EngineConfig()
+            return
         self.cfg = cfg if cfg is not None else default_config()
         h = ctypes.c_void_p()
         _check(lib().qe_engine_create(ctypes.byref(self.cfg), seed, ctypes.byref(h)), "qe_engine_create")
         self._h = h
+
+    @classmethod
+    def from_qwenbin(cls, path: str, max_seq_len: int = 0, prefill_chunk: int = 0, fused_decode: int = 1):
+        h = ctypes.c_void_p()
+        _check(lib().qe_engine_create_from_qwenbin(str(path).encode(), max_seq_len, prefill_chunk, fused_decode,
+                                                   ctypes.byref(h)), "qe_engine_create_from_qwenbin")
+        e = cls(_handle=h)
+        info = qwenbin_inspect(path)
+        c = e.cfg
+        for n in ("num_layers", "hidden_size", "intermediate_size", "num_q_heads", "num_kv_heads", "head_dim",
+                  "vocab_size"):
+            setattr(c, n, info[n])
+        c.rope_theta = info["rope_theta"]
+        fs = info["max_seq_len"] if 0 < info["max_seq_len"] <= 32768 else 4096
+        c.max_seq_len = min(max_seq_len, fs) if max_seq_len > 0 else fs
+        c.prefill_chunk = prefill_chunk if prefill_chunk > 0 else 1024
+        c.fused_decode = fused_decode
+        return e
+
+    def save_qwenbin(self, path: str):
+        _check(lib().qe_engine_save_qwenbin(self._h, str(path).encode()), "qe_engine_save_qwenbin")
 
     def close(self):
         if getattr(self, "_h", None):

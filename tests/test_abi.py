@@ -29,8 +29,11 @@ def test_library_exports_every_declared_symbol():
     launchers = [n for n in _declared() if n.startswith("qe_launch_")]
     assert sorted(launchers) == sorted(qe_amd.SIGNATURES)
     assert qe_amd.lib().qe_version().decode().startswith("qe_amd")
-    for name in _declared("qe_engine.h"):
-        assert hasattr(L, name), f"libqe_amd.so does not export {name}"
+    for header in ("qe_engine.h", "qwenbin.h"):
+        for name in _declared(header):
+            assert hasattr(L, name), f"libqe_amd.so does not export {name}"
+    assert "qe_qwenbin_inspect" in _declared("qwenbin.h")
+    assert "qe_engine_create_from_qwenbin" in _declared("qe_engine.h")
 
 
 @pytest.mark.parametrize("K", [0, 100, 129, -128])
