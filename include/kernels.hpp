@@ -32,6 +32,7 @@ constexpr int32_t KV_DIM = 256;
 constexpr int32_t VOCAB_SIZE = 151936;
 constexpr float RMS_NORM_EPS = 1e-6f;
 constexpr int32_t MAX_SEQ_LEN = 4096;
+constexpr float ROPE_THETA = 1000000.0f;
 constexpr int32_t QUANT_GROUP_SIZE = 128;
 
 // include/tensor.cuh:28-34
@@ -169,6 +170,20 @@ inline void launch_sample_and_advance(const half* logits, float* sample_scratch_
 }
 
 // ---- fused decode launchers of this build (no counterpart in kernels.cuh) ----
+inline void launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16(
+    const half* input, const half* gamma, half* output_fp16_opt, const QKVProjectionView& view, const half* q_bias,
+    const half* k_bias, const half* v_bias, half* layer_k_cache, half* layer_v_cache,
+    const DeviceControlBlock* d_control, hipStream_t stream, int hidden_size = HIDDEN_SIZE,
+    int num_q_heads = NUM_Q_HEADS, int num_kv_heads = NUM_KV_HEADS, int head_dim = HEAD_DIM,
+    int max_seq_len = MAX_SEQ_LEN, int rotary_dim = HEAD_DIM, float rope_theta = ROPE_THETA) {
+    detail::check(qe_launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16(
+                      detail::h(input), detail::h(gamma), detail::h(output_fp16_opt), detail::v(view),
+                      detail::h(q_bias), detail::h(k_bias), detail::h(v_bias), detail::h(layer_k_cache),
+                      detail::h(layer_v_cache), d_control, stream, hidden_size, num_q_heads, num_kv_heads,
+                      head_dim, max_seq_len, rotary_dim, rope_theta),
+                  "launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16");
+}
+
 inline void launch_gemv_lm_head_sample_w4a8(const uint32_t* qweight, const half* scales, const int8_t* input_q8,
                                             const float* input_scale, const int32_t* input_sum8, half* logits_opt,
                                             float* sample_scratch_val, int32_t* sample_scratch_idx,

@@ -162,6 +162,19 @@ int qe_launch_sample_and_advance(const uint16_t* logits, float* sample_scratch_v
                                  int32_t* sample_scratch_idx, qe_device_control_block* d_control,
                                  int32_t* d_mapped_pinned_token, hipStream_t stream, int vocab_size);
 
+/* RMSNorm + QKV GEMV with the bias add, NeoX RoPE and KV-cache append in the
+ * epilogue: the same results, bit for bit, as qe_launch_rmsnorm_gemv_qkv_w4a16
+ * followed by qe_launch_qkv_bias_rope_kv_append for one token (GEMV output
+ * rounded to fp16, bias added in fp16, rotation in fp32 at position
+ * d_control->seq_pos), in one launch (src/engine.cu:367-385).  head_dim 128,
+ * full rotation (rotary_dim 0 or 128), hidden_size <= 3072, 16-byte aligned
+ * buffers; no counterpart in the reference (QE_ERR_UNSUPPORTED outside). */
+int qe_launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16(
+    const uint16_t* input, const uint16_t* gamma, uint16_t* output_fp16_opt, const qe_qkv_view* view,
+    const uint16_t* q_bias, const uint16_t* k_bias, const uint16_t* v_bias, uint16_t* layer_k_cache,
+    uint16_t* layer_v_cache, const qe_device_control_block* d_control, hipStream_t stream, int hidden_size,
+    int num_q_heads, int num_kv_heads, int head_dim, int max_seq_len, int rotary_dim, float rope_theta);
+
 /* Partials written by the fused LM-head + sampling launches: the sample
  * scratch of those two entry points holds at least this many entries (the
  * reference's launch_sample_and_advance needs 256). */

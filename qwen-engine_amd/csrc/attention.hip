@@ -9,7 +9,7 @@
 // [kv_head][max_seq][head_dim] fp16 per layer; q [T][q_dim], k/v [T][kv_dim].
 // Head dim 128: one wave64 covers a head with 2 elements per lane, dot
 // products reduce with DPP/swizzle (seg_sum<64>).
-#include "qe_common.hpp"
+#include "rope_common.hpp"
 
 namespace qe {
 namespace {
@@ -87,12 +87,9 @@ __global__ __launch_bounds__(256) void qkv_bias_rope_kv_append_kernel(
     }
     float outv = static_cast<float>(xe);
     if (e < rot) {
-        const int i = e < half_rot ? e : e - half_rot;
-        const float inv_freq = exp2f(-2.0f * static_cast<float>(i) / static_cast<float>(rot) * log2f(rope_theta));
         float sn, cs;
-        sincosf(static_cast<float>(pos) * inv_freq, &sn, &cs);
-        const float x = static_cast<float>(xe), y = static_cast<float>(xp);
-        outv = e < half_rot ? x * cs - y * sn : y * sn + x * cs;  // (x0, x1) -> (x0 c - x1 s, x0 s + x1 c)
+        rope_sincos(pos, e < half_rot ? e : e - half_rot, rot, rope_theta, sn, cs);
+        outv = rope_rotate(static_cast<float>(xe), static_cast<float>(xp), e < half_rot, sn, cs);
     }
     __syncthreads();  // partners read before anyone writes
     if (!live) return;

@@ -190,19 +190,27 @@ int decode_pass(qe_engine* e, Timer* t) {
         uint16_t* kc = e->kcache + l * e->kv_stride();
         uint16_t* vc = e->vcache + l * e->kv_stride();
         const qe_qkv_view view = view_of(e, L, e->dq, e->dk, e->dv);
-        if (c.fused_decode) {
-            QE_TRY(qe_launch_rmsnorm_gemv_qkv_w4a16(e->act0, L.ln1, nullptr, &view, s, H, c.num_q_heads,
-                                                    c.num_kv_heads, c.head_dim));
+        if (c.fused_decode && H <= 3072) {  // RMSNorm + QKV + bias + RoPE + KV append in one launch
+            QE_TRY(qe_launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16(e->act0, L.ln1, nullptr, &view, L.q_bias, L.k_bias,
+                                                                   L.v_bias, kc, vc, e->ctl, s, H, c.num_q_heads,
+                                                                   c.num_kv_heads, c.head_dim, c.max_seq_len,
+                                                                   c.head_dim, c.rope_theta));
+            QE_TRY(mark(e, t, 0));
         } else {
-            QE_TRY(qe_launch_rmsnorm_q8_1(e->act0, L.ln1, nullptr, e->q8, e->q8_scale, e->q8_sum8, s, H));
-            QE_TRY(qe_launch_gemv_qkv_w4a8(&view, e->q8, e->q8_scale, e->q8_sum8, s, H, c.num_q_heads,
-                                           c.num_kv_heads, c.head_dim));
+            if (c.fused_decode) {
+                QE_TRY(qe_launch_rmsnorm_gemv_qkv_w4a16(e->act0, L.ln1, nullptr, &view, s, H, c.num_q_heads,
+                                                        c.num_kv_heads, c.head_dim));
+            } else {
+                QE_TRY(qe_launch_rmsnorm_q8_1(e->act0, L.ln1, nullptr, e->q8, e->q8_scale, e->q8_sum8, s, H));
+                QE_TRY(qe_launch_gemv_qkv_w4a8(&view, e->q8, e->q8_scale, e->q8_sum8, s, H, c.num_q_heads,
+                                               c.num_kv_heads, c.head_dim));
+            }
+            QE_TRY(mark(e, t, 0));
+            QE_TRY(qe_launch_qkv_bias_rope_kv_append(e->dq, e->dk, e->dv, L.q_bias, L.k_bias, L.v_bias, kc, vc, e->ctl,
+                                                     1, s, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_seq_len,
+                                                     c.head_dim, c.rope_theta));
+            QE_TRY(mark(e, t, 2));
         }
-        QE_TRY(mark(e, t, 0));
-        QE_TRY(qe_launch_qkv_bias_rope_kv_append(e->dq, e->dk, e->dv, L.q_bias, L.k_bias, L.v_bias, kc, vc, e->ctl, 1,
-                                                 s, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_seq_len,
-                                                 c.head_dim, c.rope_theta));
-        QE_TRY(mark(e, t, 2));
         QE_TRY(qe_launch_attention_gqa_flash_decode(e->dq, kc, vc, e->part_o, e->part_lse, e->attn, e->ctl, s,
                                                     c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_seq_len,
                                                     e->q8, e->q8_scale, e->q8_sum8));

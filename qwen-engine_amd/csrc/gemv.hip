@@ -26,6 +26,7 @@
 //     persistent blocks (grid capped per CU).
 // Shapes outside the fast kernel (weights not 16-byte aligned, K > 16384)
 // use a generic wave-per-row kernel that stages Q8_1 in LDS.
+#include "rope_common.hpp"
 #include "sample_common.hpp"
 
 namespace qe {
@@ -56,7 +57,14 @@ struct GemvParams {
     uint16_t* norm_out;     // optional fp16 normalized activation (kXRMS, block 0 writes)
     float* s_val;           // kSample: per-block best value / index
     int32_t* s_idx;
-    const qe_device_control_block* ctl;  // kSample: temperature, rng_seed, seq_pos
+    const qe_device_control_block* ctl;  // kSample: temperature, rng_seed, seq_pos; QKV rope: seq_pos
+    // QKV with rope != 0: bias, NeoX RoPE (head_dim 128) and the KV-cache append in the epilogue
+    int rope;
+    const uint16_t* bias[3];
+    uint16_t* kcache;
+    uint16_t* vcache;
+    int max_seq;
+    float rope_theta;
     int n_rows;             // physical weight rows
     int K;
 };
@@ -304,6 +312,14 @@ __device__ __forceinline__ void stage_finish_f16(const GemvParams& p, uint4 (&ra
     }
 }
 
+// QKV with RoPE: set s of block group g = s / 16 covers head g / 8; its 16
+// segments take rows j*8 + t and 64 + j*8 + t (j = g % 8, t < 8) of that head
+__device__ __forceinline__ int rope_row(int set) {
+    const int g = set >> 4, s = set & 15;
+    const int local = (s < 8) ? ((g & 7) * 8 + s) : (64 + (g & 7) * 8 + (s - 8));
+    return (g >> 3) * 128 + local;
+}
+
 template <int BT, int LPR, int NCH, int RPS, int MODE, int XM, bool LOOP>
 __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
     // SwiGLU: a segment owns a (gate, up) row pair (RPS 2), or, with 16-lane
@@ -342,11 +358,16 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
     auto load_set = [&](int st, u32x4 (&wr)[RPS][NCH], uint32_t (&hr)[RPS][NCH]) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < RPS; ++r) {
-            const int row = min(st * RPS + r, p.n_rows - 1);  // clamped: tail rows are loaded, not stored
+            int row = min(st * RPS + r, p.n_rows - 1);  // clamped: tail rows are loaded, not stored
+            int urow = min((st - seg) * RPS, p.n_rows - 1);
+            if (MODE == kQKV && p.rope) {  // segments s and s + 8 hold the rotation pair (i, i + 64) of a head
+                row = rope_row(min(st, n_sets - 1));
+                urow = row & ~127;
+            }
             const u32x4* wp;
             const uint16_t* sp;
             int m, local;
-            row_ptrs<MODE>(p, row, min((st - seg) * RPS, p.n_rows - 1), wp, sp, m, local);
+            row_ptrs<MODE>(p, row, urow, wp, sp, m, local);
 #pragma unroll
             for (int i = 0; i < NCH; ++i) {
                 const int c = min(l + i * LPR, KC - 1);
@@ -408,6 +429,39 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
             acc[r] = qwen::seg_sum<LPR>(a);
         }
         if constexpr (PAIR) acc[0] = silu_mul(acc[0], qwen::swz_xor16_f32(acc[0]));  // gate (even set) x up
+        if constexpr (MODE == kQKV && LPR == 16 && RPS == 1 && BT == 256 && !LOOP) {
+            if (p.rope) {  // block-uniform: one pass over 16-row groups of one head
+                __shared__ uint16_t s_rv[16];
+                const int row = rope_row(st);
+                const int m = (row >= p.row_begin[1]) + (row >= p.row_begin[2]);
+                const int local = row - (m == 0 ? 0 : (m == 1 ? p.row_begin[1] : p.row_begin[2]));
+                const uint16_t* b = m == 0 ? p.bias[0] : (m == 1 ? p.bias[1] : p.bias[2]);
+                // GEMV output rounded to fp16, then the bias added in fp16 (as the separate kernels do)
+                _Float16 v = static_cast<_Float16>(acc[0]);
+                if (b != nullptr) v = v + __builtin_bit_cast(_Float16, b[local]);
+                if (l == 0) s_rv[seg] = __builtin_bit_cast(uint16_t, v);
+                __syncthreads();
+                if (l == 0) {
+                    const int pos0 = p.ctl != nullptr ? p.ctl->seq_pos : 0;
+                    const int pos = pos0 < p.max_seq ? pos0 : p.max_seq - 1;
+                    const int e = local & 127, head = local >> 7;
+                    uint16_t outv = __builtin_bit_cast(uint16_t, v);
+                    if (m < 2) {  // q and k rows rotate with their partner (segment s ^ 8)
+                        float sn, cs;
+                        rope_sincos(pos, e & 63, 128, p.rope_theta, sn, cs);
+                        const float y = h2f(s_rv[seg ^ 8]);
+                        outv = f2h(rope_rotate(static_cast<float>(v), y, e < 64, sn, cs));
+                    }
+                    uint16_t* o = m == 0 ? p.out[0] : (m == 1 ? p.out[1] : p.out[2]);
+                    o[local] = outv;
+                    if (m > 0) {
+                        uint16_t* cache = m == 1 ? p.kcache : p.vcache;
+                        cache[(static_cast<size_t>(head) * p.max_seq + pos) * 128 + e] = outv;
+                    }
+                }
+                return;
+            }
+        }
         if (l == 0 && st < n_sets) {
             if constexpr (MODE == kSample) {
                 const uint16_t logit = f2h(acc[0]);
@@ -886,4 +940,39 @@ extern "C" int qe_launch_rmsnorm_gemv_lm_head_sample_w4a16(const uint16_t* input
     p.K = hidden_size;
     return launch_lm_head_sample<kXRMS>(p, sample_scratch_val, sample_scratch_idx, d_control, d_mapped_pinned_token,
                                         stream, what);
+}
+
+extern "C" int qe_launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16(
+    const uint16_t* input, const uint16_t* gamma, uint16_t* output_fp16_opt, const qe_qkv_view* view,
+    const uint16_t* q_bias, const uint16_t* k_bias, const uint16_t* v_bias, uint16_t* layer_k_cache,
+    uint16_t* layer_v_cache, const qe_device_control_block* d_control, hipStream_t stream, int hidden_size,
+    int num_q_heads, int num_kv_heads, int head_dim, int max_seq_len, int rotary_dim, float rope_theta) {
+    const char* what = "rmsnorm_gemv_qkv_rope_kv_append_w4a16";
+    if (int rc = check_k(what, hidden_size)) return rc;
+    QE_REQUIRE(input && gamma && layer_k_cache && layer_v_cache, "%s: NULL pointer", what);
+    QE_REQUIRE(head_dim == 128 && (rotary_dim == 0 || rotary_dim == 128) && max_seq_len > 0,
+               "%s: head_dim %d / rotary_dim %d (built for 128 / full rotation)", what, head_dim, rotary_dim);
+    QE_REQUIRE(hidden_size <= 3072, "%s: hidden_size %d above 3072", what, hidden_size);
+    GemvParams p{};
+    bool fast = true;
+    if (int rc = fill_qkv(p, view, num_q_heads, num_kv_heads, head_dim, fast, what)) return rc;
+    p.x16 = input;
+    p.gamma = gamma;
+    p.norm_out = output_fp16_opt;
+    p.K = hidden_size;
+    QE_REQUIRE(fast && act_fast_ok(p) && aligned(output_fp16_opt, 16), "%s: buffers must be 16-byte aligned", what);
+    p.rope = 1;
+    p.bias[0] = q_bias;
+    p.bias[1] = k_bias;
+    p.bias[2] = v_bias;
+    p.kcache = layer_k_cache;
+    p.vcache = layer_v_cache;
+    p.ctl = d_control;
+    p.max_seq = max_seq_len;
+    p.rope_theta = rope_theta;
+    const Plan pl = plan_for(p.K, p.n_rows, kQKV, true);
+    QE_REQUIRE(pl.lpr == 16 && pl.bt == 256 && pl.rps == 1 && (p.n_rows + 15) / 16 <= cu_count() * 8,
+               "%s: shape outside the single-pass kernel", what);
+    if (dispatch_fast<kQKV, kXRMS>(pl, p, stream) <= 0) return fail(QE_ERR_UNSUPPORTED, "%s: no kernel", what);
+    return check_launch(what);
 }

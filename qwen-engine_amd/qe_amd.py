@@ -35,6 +35,8 @@ SIGNATURES = {
     "qe_launch_gemm_prefill_qkv_w4a16": [_P, _P, _I, _P, _I, _I, _I, _I, _I],
     "qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _I, _P, _I, _I],
     "qe_launch_sample_and_advance": [_P, _P, _P, _P, _P, _P, _I],
+    "qe_launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                                                        _I, _I, ctypes.c_float],
     "qe_launch_gemv_lm_head_sample_w4a8": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P],
     "qe_launch_rmsnorm_gemv_lm_head_sample_w4a16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P],
     "qe_launch_rmsnorm_gemv_qkv_w4a16": [_P, _P, _P, _P, _P, _I, _I, _I, _I],
@@ -215,6 +217,16 @@ def launch_sample_and_advance(logits, sample_scratch_val, sample_scratch_idx, d_
 
 
 LM_HEAD_SAMPLE_PARTS = 2048  # QE_LM_HEAD_SAMPLE_PARTS
+
+
+def launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16(input, gamma, output_fp16_opt, view: QKVView, q_bias, k_bias,
+                                                 v_bias, layer_k_cache, layer_v_cache, d_control, stream=None,
+                                                 hidden_size=1536, num_q_heads=12, num_kv_heads=2, head_dim=128,
+                                                 max_seq_len=4096, rotary_dim=128, rope_theta=1000000.0):
+    _call("qe_launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16", _ptr(input), _ptr(gamma), _ptr(output_fp16_opt),
+          ctypes.addressof(view), _ptr(q_bias), _ptr(k_bias), _ptr(v_bias), _ptr(layer_k_cache),
+          _ptr(layer_v_cache), _ptr(d_control), _stream(stream), hidden_size, num_q_heads, num_kv_heads, head_dim,
+          max_seq_len, rotary_dim, rope_theta)
 
 
 # ---- fused decode entry points (no counterpart in the reference API) ---------

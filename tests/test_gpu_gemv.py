@@ -237,3 +237,40 @@ def test_gemv_two_rows_per_segment_tails(qe, orc, N):
     got = _gemv_w4a8(qe, qw, sc, q8, xs, s8, N, K)
     ref, ex, bd = orc.gemv_w4a8(qw, sc, q8, xs, s8, N, K)
     assert_fp16_close(got, ex, bd, ref, what=f"rps2 N={N}")
+
+
+@pytest.mark.parametrize("H,nq,nkv,pos", [(1536, 12, 2, 0), (1536, 12, 2, 777), (256, 2, 1, 4095)])
+def test_fused_qkv_rope_kv_append_bit_identical(qe, orc, H, nq, nkv, pos):
+    """RMSNorm + QKV GEMV with bias + RoPE + KV append in the epilogue equals,
+    bit for bit, the two launches it replaces (rmsnorm_gemv_qkv_w4a16 then
+    qkv_bias_rope_kv_append)."""
+    hd, max_seq = 128, 4096
+    dims = (nq * hd, nkv * hd, nkv * hd)
+    mats = [orc.synth_w4(700 + i, n, H) for i, n in enumerate(dims)]
+    x16 = (orc.synth_f16_normal(7, H).astype(np.float32) * 2).astype(np.float16)
+    g16 = (1 + 0.2 * orc.synth_f16_normal(8, H).astype(np.float32)).astype(np.float16)
+    rng = np.random.default_rng(pos)
+    biases = [dev((rng.standard_normal(n) * 0.1).astype(np.float16)) for n in dims]
+    dw = [(dev(w), dev(s)) for w, s in mats]
+    raw = np.zeros(64, np.int32)
+    raw[1] = pos
+    ctl = dev(raw)
+    results = []
+    for fused in (True, False):
+        outs = [empty(n, torch.float16) for n in dims]
+        kc = torch.zeros((nkv, max_seq, hd), dtype=torch.float16, device="cuda")
+        vc = torch.zeros((nkv, max_seq, hd), dtype=torch.float16, device="cuda")
+        view = qe.make_qkv_view(dw[0][0], dw[0][1], outs[0], dw[1][0], dw[1][1], outs[1], dw[2][0], dw[2][1], outs[2])
+        if fused:
+            qe.launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16(dev(x16), dev(g16), None, view, biases[0], biases[1],
+                                                            biases[2], kc, vc, ctl, hidden_size=H, num_q_heads=nq,
+                                                            num_kv_heads=nkv, head_dim=hd, max_seq_len=max_seq)
+        else:
+            qe.launch_rmsnorm_gemv_qkv_w4a16(dev(x16), dev(g16), None, view, hidden_size=H, num_q_heads=nq,
+                                             num_kv_heads=nkv, head_dim=hd)
+            qe.launch_qkv_bias_rope_kv_append(outs[0], outs[1], outs[2], biases[0], biases[1], biases[2], kc, vc, ctl,
+                                              1, num_q_heads=nq, num_kv_heads=nkv, head_dim=hd, max_seq_len=max_seq)
+        results.append([host(o).view(np.uint16) for o in outs] + [host(kc).view(np.uint16), host(vc).view(np.uint16)])
+    for a, b, name in zip(results[0], results[1], ("q", "k", "v", "k_cache", "v_cache")):
+        assert np.array_equal(a, b), name
+    assert np.any(results[0][3][:, pos] != 0)  # the cache row was written
