@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstring>
 #include <random>
+#include <thread>
 #include <vector>
 #include <algorithm>
 
@@ -264,6 +265,27 @@ void oracle_gemv_swiglu_w4a8(const uint32_t* qw, const uint16_t* scales,
         // |d(silu(g)u)| <= |u|*|dg|*1.1 + |silu(g)|*|du|
         if (abs_bound) abs_bound[r] = 1.1 * std::fabs(u) * bg + std::fabs(g) * bu;
     }
+}
+
+// The same rows split over `threads` host threads (contiguous row ranges):
+// the multi-core form of the CPU golden, for the bench's CPU baseline.
+void oracle_gemv_swiglu_w4a8_mt(const uint32_t* qw, const uint16_t* scales, const int8_t* q8, const float* xs,
+                                const int32_t* sum8, uint16_t* out, int K, int I, int threads) {
+    if (threads < 1) threads = 1;
+    std::vector<std::thread> pool;
+    for (int t = 0; t < threads; ++t) {
+        const int r0 = static_cast<int>(static_cast<long long>(I) * t / threads);
+        const int r1 = static_cast<int>(static_cast<long long>(I) * (t + 1) / threads);
+        pool.emplace_back([=] {
+            for (int r = r0; r < r1; ++r) {
+                double bg = 0.0, bu = 0.0;
+                const double g = eval_row(qw, scales, q8, xs, sum8, 2 * r, K, &bg);
+                const double u = eval_row(qw, scales, q8, xs, sum8, 2 * r + 1, K, &bu);
+                out[r] = f64_to_f16(silu_times(g, u));
+            }
+        });
+    }
+    for (auto& th : pool) th.join();
 }
 
 void oracle_gemv_w4a16(const uint32_t* qw, const uint16_t* scales, const uint16_t* x,

@@ -71,6 +71,10 @@ void oracle_gemm_swiglu_w4a16(const uint32_t* qw, const uint16_t* scales, const 
                               uint16_t* out, int M, int K, int I,
                               double* out_exact, double* abs_bound);
 
+/* oracle_gemv_swiglu_w4a8's fp16 outputs computed by `threads` host threads. */
+void oracle_gemv_swiglu_w4a8_mt(const uint32_t* qw, const uint16_t* scales, const int8_t* q8, const float* xs,
+                                const int32_t* sum8, uint16_t* out, int K, int I, int threads);
+
 /* RMSNorm of the reference kernels: fp16(fp16(x * fp16(inv_rms)) * gamma). */
 void oracle_rmsnorm_fp16(const uint16_t* x, const uint16_t* gamma, uint16_t* out,
                          int num_tokens, int H, float eps);

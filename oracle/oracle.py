@@ -54,6 +54,7 @@ def lib():
             "oracle_rmsnorm_fp16": [_P, _P, _P, _I, _I, ctypes.c_float],
             "oracle_argmax_f16": [_P, _I],
             "oracle_philox4x32_10": [_P, _P, _P],
+            "oracle_gemv_swiglu_w4a8_mt": [_P, _P, _P, _P, _P, _P, _I, _I, _I],
             "oracle_suite3_inputs": [_I, _I, _P, _P, _P],
             "oracle_synth_w4": [ctypes.c_uint64, _I, _I, _P, _P],
             "oracle_synth_f16_normal": [ctypes.c_uint64, _I64, _P],
@@ -241,6 +242,15 @@ def rmsnorm_fp16(x, gamma, eps=1e-6):
 def argmax_f16(logits) -> int:
     logits = _c(logits, np.float16)
     return int(lib().oracle_argmax_f16(_p(logits), logits.size))
+
+
+def gemv_swiglu_w4a8_mt(qw, scales, q8, xs, s8, K, I, threads):
+    """fp16 outputs of gemv_swiglu_w4a8, rows split over host threads."""
+    qw, scales = _c(qw, np.uint32), _c(scales, np.float16)
+    q8, xs, s8 = _c(q8, np.int8), _c(xs, np.float32), _c(s8, np.int32)
+    out = np.empty(I, np.float16)
+    lib().oracle_gemv_swiglu_w4a8_mt(_p(qw), _p(scales), _p(q8), _p(xs), _p(s8), _p(out), K, I, threads)
+    return out
 
 
 def philox4x32_10(ctr, key):

@@ -351,3 +351,14 @@ def test_gumbel_sampling_follows_softmax(orc):
     # temperature <= 1e-5 is greedy
     tok, vals = orc.sample_f16(logits, 1e-6, 42, 3)
     assert tok == 0 and np.array_equal(vals, logits.astype(np.float32))
+
+
+def test_multithreaded_swiglu_gemv_matches_scalar(orc):
+    """The multi-core CPU baseline computes the same fp16 outputs as the scalar golden."""
+    qw, sc = orc.synth_w4(17, 2 * 384, 1536)
+    x = orc.synth_f16_normal(18, 1536)
+    q8, xs, s8 = orc.quantize_q8_1(x)
+    ref = orc.gemv_swiglu_w4a8(qw, sc, q8, xs, s8, 1536, 384)[0]
+    for threads in (1, 3, 8):
+        got = orc.gemv_swiglu_w4a8_mt(qw, sc, q8, xs, s8, 1536, 384, threads)
+        assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
