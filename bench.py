@@ -349,6 +349,28 @@ def main():
             del qw, sc
         pre.append({"M": M, "shape": "layer total", "TFLOP/s": round(tot_flop / (tot_ms * 1e-3) / 1e12, 1),
                     "mfma_frac": round(tot_flop / (tot_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)})
+        # int8-MFMA variant (W4A8: activation rows quantized to Q8_1 first, quantization included)
+        q8p = torch.empty(M * I, dtype=torch.int8, device=dev)
+        xsp = torch.empty(M * I // 128, dtype=torch.float32, device=dev)
+        s8p = torch.empty(M * I // 8, dtype=torch.int32, device=dev)
+        tot8 = 0.0
+        for (N, K, name) in ((2048, H, "qkv"), (H, H, "o"), (2 * I, H, "gate_up"), (H, I, "down")):
+            C = max(2, min(64, copies_for(N * K // 2)))
+            qw, sc = rand_w4(N, K, C)
+
+            def fn8(i, qw=qw, sc=sc, N=N, K=K, name=name):
+                qe_amd.launch_quantize_fp16_to_q8_1(A, q8p, xsp, s8p, M * K)
+                if name == "gate_up":
+                    qe_amd.launch_gemm_prefill_dual_gate_up_swiglu_w4a8(qw[i % C], sc[i % C], q8p, xsp, s8p, outp, M,
+                                                                        hidden_size=K, intermediate_size=I)
+                else:
+                    qe_amd.launch_gemm_prefill_w4a8(qw[i % C], sc[i % C], q8p, xsp, s8p, None, outp, M, N, K)
+
+            tot8 += time_graph(graph_of(fn8, C), 3) / C
+            del qw, sc
+        pre.append({"M": M, "shape": "layer total, int8 MFMA (W4A8, incl. Q8_1 quantization)",
+                    "TFLOP/s": round(tot_flop / (tot8 * 1e-3) / 1e12, 1),
+                    "mfma_frac_int8_peak": round(tot_flop / (tot8 * 1e-3) / 1e12 / (2 * MFMA_F16_PEAK_TFLOPS), 4)})
     result["prefill_gemm"] = pre
 
     # ---------------- end-to-end decode -------------------------

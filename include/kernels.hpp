@@ -169,6 +169,37 @@ inline void launch_sample_and_advance(const half* logits, float* sample_scratch_
                   "launch_sample_and_advance");
 }
 
+// ---- W4A8 prefill GEMM of this build (int8 MFMA; no counterpart in kernels.cuh) ----
+inline void launch_gemm_prefill_w4a8(const uint32_t* qweight, const half* scales, const int8_t* input_q8,
+                                     const float* input_scale, const int32_t* input_sum8, const half* residual,
+                                     half* output_y, int M, int N, int K, hipStream_t stream) {
+    detail::check(qe_launch_gemm_prefill_w4a8(qweight, detail::h(scales), input_q8, input_scale, input_sum8,
+                                              detail::h(residual), detail::h(output_y), M, N, K, stream),
+                  "launch_gemm_prefill_w4a8");
+}
+
+inline void launch_gemm_prefill_qkv_w4a8(const QKVProjectionView& view, const int8_t* input_q8,
+                                         const float* input_scale, const int32_t* input_sum8, int M,
+                                         hipStream_t stream, int in_features = HIDDEN_SIZE,
+                                         int num_q_heads = NUM_Q_HEADS, int num_kv_heads = NUM_KV_HEADS,
+                                         int head_dim = HEAD_DIM) {
+    detail::check(qe_launch_gemm_prefill_qkv_w4a8(detail::v(view), input_q8, input_scale, input_sum8, M, stream,
+                                                  in_features, num_q_heads, num_kv_heads, head_dim),
+                  "launch_gemm_prefill_qkv_w4a8");
+}
+
+inline void launch_gemm_prefill_dual_gate_up_swiglu_w4a8(const uint32_t* gate_up_qweight, const half* gate_up_scales,
+                                                         const int8_t* input_q8, const float* input_scale,
+                                                         const int32_t* input_sum8, half* output_mlp, int M,
+                                                         hipStream_t stream, int hidden_size = HIDDEN_SIZE,
+                                                         int intermediate_size = INTERMEDIATE_SIZE) {
+    detail::check(qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a8(gate_up_qweight, detail::h(gate_up_scales),
+                                                                  input_q8, input_scale, input_sum8,
+                                                                  detail::h(output_mlp), M, stream, hidden_size,
+                                                                  intermediate_size),
+                  "launch_gemm_prefill_dual_gate_up_swiglu_w4a8");
+}
+
 // ---- fused decode launchers of this build (no counterpart in kernels.cuh) ----
 inline void launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16(
     const half* input, const half* gamma, half* output_fp16_opt, const QKVProjectionView& view, const half* q_bias,

@@ -162,6 +162,26 @@ int qe_launch_sample_and_advance(const uint16_t* logits, float* sample_scratch_v
                                  int32_t* sample_scratch_idx, qe_device_control_block* d_control,
                                  int32_t* d_mapped_pinned_token, hipStream_t stream, int vocab_size);
 
+/* W4A8 prefill GEMM on the int8 matrix cores (v_mfma_i32_32x32x32_i8): the
+ * activation rows enter as Q8_1 (input_q8 [M][K], input_scale [M][K/128],
+ * input_sum8 [M][K/8], e.g. qe_launch_quantize_fp16_to_q8_1 over M*K
+ * elements), so every output row is the W4A8 GEMV of that row
+ * (gemv_w4a16.cu:74-121 math, integer group dots exact, fp32 scale and
+ * accumulation, fp16 out; residual added as fp16(fp16(acc) + res) like the
+ * fp16 GEMM).  The int8 prefill alternative named in design_draft.md:117-120
+ * of the reference; no counterpart in its API.  K % 128 == 0, 16-byte
+ * aligned Q8_1 rows and weights. */
+int qe_launch_gemm_prefill_w4a8(const uint32_t* qweight, const uint16_t* scales, const int8_t* input_q8,
+                                const float* input_scale, const int32_t* input_sum8, const uint16_t* residual,
+                                uint16_t* output_y, int M, int N, int K, hipStream_t stream);
+int qe_launch_gemm_prefill_qkv_w4a8(const qe_qkv_view* view, const int8_t* input_q8, const float* input_scale,
+                                    const int32_t* input_sum8, int M, hipStream_t stream, int in_features,
+                                    int num_q_heads, int num_kv_heads, int head_dim);
+int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a8(const uint32_t* gate_up_qweight, const uint16_t* gate_up_scales,
+                                                    const int8_t* input_q8, const float* input_scale,
+                                                    const int32_t* input_sum8, uint16_t* output_mlp, int M,
+                                                    hipStream_t stream, int hidden_size, int intermediate_size);
+
 /* RMSNorm + QKV GEMV with the bias add, NeoX RoPE and KV-cache append in the
  * epilogue: the same results, bit for bit, as qe_launch_rmsnorm_gemv_qkv_w4a16
  * followed by qe_launch_qkv_bias_rope_kv_append for one token (GEMV output

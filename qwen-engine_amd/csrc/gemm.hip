@@ -31,6 +31,7 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPlain = 0;
 constexpr int kQKV = 1;
@@ -46,6 +47,9 @@ struct GemmParams {
     int out_stride[3]; // row stride of each output
     const uint16_t* A;
     const uint16_t* residual;
+    const int8_t* A8;         // W4A8 variant: Q8_1 rows of the activation
+    const float* A8_scale;
+    const int32_t* A8_sum8;
     int M, N, K;       // N = virtual columns (SwiGLU: 2*I)
 };
 
@@ -384,6 +388,184 @@ int launch_gemm(const GemmParams& p, hipStream_t stream, const char* what) {
     return check_launch(what);
 }
 
+// ---- W4A8 variant: int8 activations on the int8 matrix cores ----------------------
+// v_mfma_i32_32x32x32_i8 takes 16 int8 k per lane; within one 128-group a
+// lane half h covers k in [64h, 64h + 64), 16 per MFMA j (k = 64h + 16j), for
+// both operands.  The weights enter as their unsigned nibbles q (two ops per
+// 4 bytes: & 0x0F0F0F0F and >> 4); sum (q - 8) a = sum q a + the Q8_1 sum8
+// terms (-8 * sum a per 8 elements), so the correction per row and group is
+// the sum of its 16 sum8 words.  Per group: 4 MFMAs into an int32 tile from
+// zero, then fp32 += float(int dot + correction) * (w_scale * x_scale) - the
+// GEMV's per-chunk arithmetic with the four chunk dots summed first (integer
+// addition; evaluated as w_s * (float(dot) * x_s + float(corr) * x_s), two
+// fused multiply-adds per element and group).  A (Q8_1 int8 rows) and the
+// per-row group scale/correction go through LDS; weights straight from
+// global as in the fp16 kernel; K split into slices when the tile grid leaves
+// CUs idle (partials reduced by the fp16 kernel's reduce pass).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+constexpr int A8_STRIDE = 144;  // bytes per LDS row of the int8 A tile (128 + 16 pad)
+
+template <int BM, int MODE>
+__global__ __launch_bounds__(256, 2) void gemm_w4a8_mfma_kernel(GemmParams p) {
+    constexpr int BN = 128, WGM = 1, MI = BM / 32;
+    constexpr int A_U = BM / 32;  // 16-byte A chunks per thread per step: 8 threads per 128-byte row, 32 rows per pass
+    constexpr int D = 2;          // stages of the register ring
+    __shared__ __align__(16) int8_t sA[2][BM * A8_STRIDE];
+    __shared__ __align__(16) float s_xs[2][BM];
+    __shared__ __align__(16) float s_cr[2][BM];  // float(correction) * x_scale
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wn = tid >> 6;
+    const int m0 = blockIdx.y * BM;
+    const int n0 = blockIdx.x * BN;
+    const int K = p.K;
+    const int G = K >> 7;
+    const int slices = gridDim.z;
+    const int g_begin = static_cast<int>((static_cast<long long>(blockIdx.z) * G) / slices);
+    const int g_end = static_cast<int>((static_cast<long long>(blockIdx.z + 1) * G) / slices);
+    const int KT = g_end - g_begin;  // one 128-group per step
+    const int fr = lane & 31;
+    const int h = lane >> 5;
+
+    const int a_row = tid >> 3, a_c = tid & 7;
+    const int8_t* a_src[A_U];
+#pragma unroll
+    for (int i = 0; i < A_U; ++i)
+        a_src[i] = p.A8 + static_cast<size_t>(min(m0 + a_row + 32 * i, p.M - 1)) * K + 16 * a_c;
+    const int srow = tid % BM;  // row whose group scale / correction this thread fetches
+    const size_t srow_g = static_cast<size_t>(min(m0 + srow, p.M - 1));
+    // B: the lane's column; columns past N read column N-1
+    const int col = min(n0 + wn * 32 + fr, p.N - 1);
+    int m = 0, local = col;
+    if constexpr (MODE == kQKV) {
+        m = (col >= p.col_begin[1]) + (col >= p.col_begin[2]);
+        local = col - p.col_begin[m];
+    }
+    const u32x4* b_src = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(local) * (K >> 3)) + 2 * h;
+    const uint16_t* b_sc = p.sc[m] + static_cast<size_t>(local) * G;
+
+    struct Stage {
+        i32x4 a[A_U];
+        float xs;
+        i32x4 s8[4];
+        u32x4 b[2];
+        uint32_t bs;
+    };
+    Stage st[D];
+    auto load = [&](int kt, Stage& S) __attribute__((always_inline)) {
+        const int g = g_begin + kt;
+#pragma unroll
+        for (int i = 0; i < A_U; ++i) S.a[i] = *reinterpret_cast<const i32x4*>(a_src[i] + g * 128);
+        S.xs = p.A8_scale[srow_g * G + g];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            S.s8[j] = *reinterpret_cast<const i32x4*>(p.A8_sum8 + srow_g * (K >> 3) + 16 * g + 4 * j);
+        S.b[0] = __builtin_nontemporal_load(b_src + 4 * g);
+        S.b[1] = __builtin_nontemporal_load(b_src + 4 * g + 1);
+        S.bs = b_sc[g];
+    };
+    auto store = [&](int buf, const Stage& S) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < A_U; ++i)
+            *reinterpret_cast<i32x4*>(&sA[buf][(a_row + 32 * i) * A8_STRIDE + 16 * a_c]) = S.a[i];
+        int cr = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cr += S.s8[j].x + S.s8[j].y + S.s8[j].z + S.s8[j].w;
+        s_xs[buf][srow] = S.xs;  // threads srow and srow + BM write the same values
+        s_cr[buf][srow] = static_cast<float>(cr) * S.xs;
+    };
+
+    f32x16 f[MI][1];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) f[i][0] = f32x16{};
+
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(min(d, KT - 1), st[d]);
+    store(0, st[0]);
+    __syncthreads();
+
+    auto step = [&](int kt, int d) __attribute__((always_inline)) {
+        const int buf = kt & 1;
+        const Stage& S = st[d];
+        i32x16 acc[MI];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t w0 = S.b[j >> 1][(2 * j) & 3], w1 = S.b[j >> 1][(2 * j + 1) & 3];
+            const i32x4 bop = {static_cast<int>(w0 & 0x0F0F0F0Fu), static_cast<int>((w0 >> 4) & 0x0F0F0F0Fu),
+                               static_cast<int>(w1 & 0x0F0F0F0Fu), static_cast<int>((w1 >> 4) & 0x0F0F0F0Fu)};
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const i32x4 aop =
+                    *reinterpret_cast<const i32x4*>(&sA[buf][(i * 32 + fr) * A8_STRIDE + 64 * h + 16 * j]);
+                acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, j == 0 ? i32x16{} : acc[i], 0, 0, 0);
+            }
+        }
+        const float ws = h2f(static_cast<uint16_t>(S.bs));
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+#pragma unroll
+            for (int v4 = 0; v4 < 4; ++v4) {
+                const int r0 = i * 32 + 8 * v4 + 4 * h;  // rows r0..r0+3 hold elements 4*v4 .. 4*v4+3
+                const f32x4 xs4 = *reinterpret_cast<const f32x4*>(&s_xs[buf][r0]);
+                const f32x4 cr4 = *reinterpret_cast<const f32x4*>(&s_cr[buf][r0]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {  // f += w_s * (float(dot) * x_s + float(corr) * x_s)
+                    const int v = 4 * v4 + q;
+                    f[i][0][v] = fmaf(ws, fmaf(static_cast<float>(acc[i][v]), xs4[q], cr4[q]), f[i][0][v]);
+                }
+            }
+        }
+        load(min(kt + D, KT - 1), st[d]);  // step kt is consumed: refill with step kt + D
+        store(buf ^ 1, st[(d + 1) % D]);   // step kt + 1, loaded D - 1 steps ago
+        __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + D <= KT; kt += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) step(kt + d, d);
+    }
+    if (kt < KT) step(kt, 0);  // tail (D = 2)
+    if (slices == 1) {
+        epilogue<BM, BN, WGM, MODE>(p, f, m0, n0, 0, wn, lane);
+        return;
+    }
+    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const int n_tiles = gridDim.x * gridDim.y;
+    float* mine = g_splitk_ws + (static_cast<size_t>(blockIdx.z) * n_tiles + tile) * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mine[(i * 16 + v) * 256 + tid] = f[i][0][v];
+}
+
+template <int MODE>
+int launch_gemm_w4a8(const GemmParams& p, hipStream_t stream, const char* what) {
+    if (p.M <= 0 || p.N <= 0) return QE_OK;
+    // 128-row tiles when they already give one block per CU, else 64-row tiles
+    const int cus = cu_count();
+    const int nt128 = ((p.M + 127) / 128) * ((p.N + 127) / 128);
+    const bool big = nt128 >= cus;
+    const int bm = big ? 128 : 64;
+    if ((p.M + bm - 1) / bm > 65535) return fail(QE_ERR_UNSUPPORTED, "%s: M=%d too large", what, p.M);
+    const dim3 grid((p.N + 127) / 128, (p.M + bm - 1) / bm);
+    const int tiles = static_cast<int>(grid.x * grid.y);
+    const int G = p.K / 128;
+    int slices = 1;  // about two blocks per CU, >= 4 groups per slice
+    if (tiles < cus && gemm_split_k_enabled()) slices = std::max(1, std::min((2 * cus + tiles - 1) / tiles, G / 4));
+    if (const int f = gemm_forced_slices()) slices = std::max(1, std::min(f, G));
+    while (slices > 1 && static_cast<size_t>(slices) * tiles * bm * 128 > kWsFloats) --slices;
+    const dim3 g3(grid.x, grid.y, slices);
+    if (big) gemm_w4a8_mfma_kernel<128, MODE><<<g3, 256, 0, stream>>>(p);
+    else gemm_w4a8_mfma_kernel<64, MODE><<<g3, 256, 0, stream>>>(p);
+    if (slices > 1) {
+        if (big) gemm_splitk_reduce_kernel<128, 128, 1, MODE><<<grid, 256, 0, stream>>>(p, slices);
+        else gemm_splitk_reduce_kernel<64, 128, 1, MODE><<<grid, 256, 0, stream>>>(p, slices);
+    }
+    return check_launch(what);
+}
+
 int check_gemm_common(const char* what, const uint16_t* A, int M, int K) {
     QE_REQUIRE(A != nullptr, "%s: input_x is NULL", what);
     QE_REQUIRE(M >= 0, "%s: M=%d", what, M);
@@ -474,4 +656,99 @@ extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(const uint32_t* 
     p.N = 2 * intermediate_size;
     p.K = hidden_size;
     return launch_gemm<kSwiglu>(p, stream, what);
+}
+
+// ---- W4A8 prefill GEMM entry points --------------------------------------------------
+namespace {
+int check_gemm_a8(const char* what, const int8_t* q8, const float* xs, const int32_t* s8, int M, int K) {
+    QE_REQUIRE(q8 && xs && s8, "%s: Q8_1 input pointers must not be NULL", what);
+    QE_REQUIRE(M >= 0, "%s: M=%d", what, M);
+    QE_REQUIRE(K > 0 && K % 128 == 0, "%s: K=%d must be a positive multiple of 128", what, K);
+    QE_REQUIRE(aligned(q8, 16) && aligned(s8, 16) && aligned(xs, 4), "%s: Q8_1 rows must be 16-byte aligned", what);
+    return QE_OK;
+}
+}  // namespace
+
+extern "C" int qe_launch_gemm_prefill_w4a8(const uint32_t* qweight, const uint16_t* scales, const int8_t* input_q8,
+                                           const float* input_scale, const int32_t* input_sum8,
+                                           const uint16_t* residual, uint16_t* output_y, int M, int N, int K,
+                                           hipStream_t stream) {
+    const char* what = "gemm_prefill_w4a8";
+    if (int rc = check_gemm_a8(what, input_q8, input_scale, input_sum8, M, K)) return rc;
+    QE_REQUIRE(qweight && scales && output_y && N >= 0, "%s: NULL weight/scale/output or N < 0", what);
+    QE_REQUIRE(aligned(qweight, 16) && aligned(scales, 2), "%s: qweight must be 16-byte aligned", what);
+    GemmParams p{};
+    p.qw[0] = qweight;
+    p.sc[0] = scales;
+    p.out[0] = output_y;
+    p.out_stride[0] = N;
+    p.A8 = input_q8;
+    p.A8_scale = input_scale;
+    p.A8_sum8 = input_sum8;
+    p.residual = residual;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    return launch_gemm_w4a8<kPlain>(p, stream, what);
+}
+
+extern "C" int qe_launch_gemm_prefill_qkv_w4a8(const qe_qkv_view* view, const int8_t* input_q8,
+                                               const float* input_scale, const int32_t* input_sum8, int M,
+                                               hipStream_t stream, int in_features, int num_q_heads,
+                                               int num_kv_heads, int head_dim) {
+    const char* what = "gemm_prefill_qkv_w4a8";
+    if (int rc = check_gemm_a8(what, input_q8, input_scale, input_sum8, M, in_features)) return rc;
+    QE_REQUIRE(view != nullptr, "%s: view is NULL", what);
+    QE_REQUIRE(num_q_heads >= 0 && num_kv_heads >= 0 && head_dim >= 0, "%s: negative head shape", what);
+    const int q_dim = num_q_heads * head_dim;
+    const int kv_dim = num_kv_heads * head_dim;
+    const void* w[3] = {view->q_weight, view->k_weight, view->v_weight};
+    const uint16_t* s[3] = {view->q_scale, view->k_scale, view->v_scale};
+    uint16_t* o[3] = {view->d_q, view->d_k, view->d_v};
+    const int cols[3] = {q_dim, kv_dim, kv_dim};
+    GemmParams p{};
+    for (int i = 0; i < 3; ++i) {
+        p.out_stride[i] = cols[i];
+        if (cols[i] == 0) continue;
+        QE_REQUIRE(w[i] && s[i] && o[i], "%s: NULL pointer in view (matrix %d)", what, i);
+        QE_REQUIRE(aligned(w[i], 16) && aligned(s[i], 2), "%s: weights must be 16-byte aligned", what);
+        p.qw[i] = static_cast<const uint32_t*>(w[i]);
+        p.sc[i] = s[i];
+        p.out[i] = o[i];
+    }
+    p.col_begin[0] = 0;
+    p.col_begin[1] = q_dim;
+    p.col_begin[2] = q_dim + kv_dim;
+    p.A8 = input_q8;
+    p.A8_scale = input_scale;
+    p.A8_sum8 = input_sum8;
+    p.M = M;
+    p.N = q_dim + 2 * kv_dim;
+    p.K = in_features;
+    return launch_gemm_w4a8<kQKV>(p, stream, what);
+}
+
+extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a8(const uint32_t* gate_up_qweight,
+                                                               const uint16_t* gate_up_scales,
+                                                               const int8_t* input_q8, const float* input_scale,
+                                                               const int32_t* input_sum8, uint16_t* output_mlp, int M,
+                                                               hipStream_t stream, int hidden_size,
+                                                               int intermediate_size) {
+    const char* what = "gemm_prefill_dual_gate_up_swiglu_w4a8";
+    if (int rc = check_gemm_a8(what, input_q8, input_scale, input_sum8, M, hidden_size)) return rc;
+    QE_REQUIRE(gate_up_qweight && gate_up_scales && output_mlp && intermediate_size >= 0, "%s: bad arguments", what);
+    QE_REQUIRE(aligned(gate_up_qweight, 16) && aligned(gate_up_scales, 2), "%s: qweight must be 16-byte aligned",
+               what);
+    GemmParams p{};
+    p.qw[0] = gate_up_qweight;
+    p.sc[0] = gate_up_scales;
+    p.out[0] = output_mlp;
+    p.out_stride[0] = intermediate_size;
+    p.A8 = input_q8;
+    p.A8_scale = input_scale;
+    p.A8_sum8 = input_sum8;
+    p.M = M;
+    p.N = 2 * intermediate_size;
+    p.K = hidden_size;
+    return launch_gemm_w4a8<kSwiglu>(p, stream, what);
 }

@@ -35,6 +35,9 @@ SIGNATURES = {
     "qe_launch_gemm_prefill_qkv_w4a16": [_P, _P, _I, _P, _I, _I, _I, _I, _I],
     "qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _I, _P, _I, _I],
     "qe_launch_sample_and_advance": [_P, _P, _P, _P, _P, _P, _I],
+    "qe_launch_gemm_prefill_w4a8": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "qe_launch_gemm_prefill_qkv_w4a8": [_P, _P, _P, _P, _I, _P, _I, _I, _I, _I],
+    "qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a8": [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I],
     "qe_launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
                                                         _I, _I, ctypes.c_float],
     "qe_launch_gemv_lm_head_sample_w4a8": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P],
@@ -217,6 +220,26 @@ def launch_sample_and_advance(logits, sample_scratch_val, sample_scratch_idx, d_
 
 
 LM_HEAD_SAMPLE_PARTS = 2048  # QE_LM_HEAD_SAMPLE_PARTS
+
+
+def launch_gemm_prefill_w4a8(qweight, scales, input_q8, input_scale, input_sum8, residual, output_y, M, N, K,
+                             stream=None):
+    _call("qe_launch_gemm_prefill_w4a8", _ptr(qweight), _ptr(scales), _ptr(input_q8), _ptr(input_scale),
+          _ptr(input_sum8), _ptr(residual), _ptr(output_y), M, N, K, _stream(stream))
+
+
+def launch_gemm_prefill_qkv_w4a8(view: QKVView, input_q8, input_scale, input_sum8, M, stream=None, in_features=1536,
+                                 num_q_heads=12, num_kv_heads=2, head_dim=128):
+    _call("qe_launch_gemm_prefill_qkv_w4a8", ctypes.addressof(view), _ptr(input_q8), _ptr(input_scale),
+          _ptr(input_sum8), M, _stream(stream), in_features, num_q_heads, num_kv_heads, head_dim)
+
+
+def launch_gemm_prefill_dual_gate_up_swiglu_w4a8(gate_up_qweight, gate_up_scales, input_q8, input_scale,
+                                                 input_sum8, output_mlp, M, stream=None, hidden_size=1536,
+                                                 intermediate_size=8960):
+    _call("qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a8", _ptr(gate_up_qweight), _ptr(gate_up_scales),
+          _ptr(input_q8), _ptr(input_scale), _ptr(input_sum8), _ptr(output_mlp), M, _stream(stream), hidden_size,
+          intermediate_size)
 
 
 def launch_rmsnorm_gemv_qkv_rope_kv_append_w4a16(input, gamma, output_fp16_opt, view: QKVView, q_bias, k_bias,

@@ -148,3 +148,73 @@ def test_gemm_split_k_deterministic_across_interleaved_launches(qe, orc):
     for i, (dqw, dsc, dA, out, M, N, K, qw, sc, A) in enumerate(data):
         ref, ex, bd = orc.gemm_w4a16(qw, sc, A, M, N, K)
         assert_fp16_close(first[i], ex, bd, ref, what=f"split-K shape {i}")
+
+
+# ---- W4A8 prefill GEMM (int8 MFMA) ------------------------------------------------
+def _q8_rows(qe, A):
+    M, K = A.shape
+    q8, xs, s8 = empty(M * K, torch.int8), empty(M * K // 128, torch.float32), empty(M * K // 8, torch.int32)
+    qe.launch_quantize_fp16_to_q8_1(dev(A.reshape(-1)), q8, xs, s8, M * K)
+    return q8, xs, s8
+
+
+def _rows_ref(orc, qw, sc, q8, xs, s8, rows, N, K, residual=None):
+    hq, hx, hs = host(q8).reshape(-1, K), host(xs).reshape(-1, K // 128), host(s8).reshape(-1, K // 8)
+    out = []
+    for m in rows:
+        out.append(orc.gemv_w4a8(qw, sc, hq[m], hx[m], hs[m], N, K,
+                                 residual=None if residual is None else residual[m]))
+    return [np.stack(t) for t in zip(*out)]
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 128), (37, 200, 256), (128, 1536, 1536), (300, 130, 384),
+                                   (64, 1536, 8960), (129, 2048, 1536), (1024, 1536, 1536)])
+def test_gemm_w4a8_rows_equal_w4a8_gemv(qe, orc, M, N, K):
+    """Every output row of the int8-MFMA GEMM is the W4A8 GEMV of that row's
+    Q8_1 (the activation quantized by the bit-exact quantizer)."""
+    print(f"gemm_w4a8 M={M} N={N} K={K}", flush=True)
+    qw, sc = orc.synth_w4(M + 3 * N + K, N, K)
+    A = _A(orc, M, K, 15)
+    q8, xs, s8 = _q8_rows(qe, A)
+    out = empty((M, N), torch.float16)
+    qe.launch_gemm_prefill_w4a8(dev(qw), dev(sc), q8, xs, s8, None, out, M, N, K)
+    rows = list(range(M)) if M <= 130 else sorted(set([0, 1, M // 2, M - 2, M - 1] + list(range(60, 70))))
+    ref, ex, bd = _rows_ref(orc, qw, sc, q8, xs, s8, rows, N, K)
+    assert_fp16_close(host(out)[rows], ex, bd, ref, what=f"gemm_w4a8 {M}x{N}x{K}")
+
+
+def test_gemm_w4a8_residual_qkv_swiglu(qe, orc):
+    M, H, I = 96, 1536, 512
+    A = _A(orc, M, H, 16)
+    q8, xs, s8 = _q8_rows(qe, A)
+    from helpers import ulp16
+    # residual in place
+    qw, sc = orc.synth_w4(90, H, H)
+    R = orc.synth_f16_normal(91, M * H).reshape(M, H)
+    out = dev(R)
+    qe.launch_gemm_prefill_w4a8(dev(qw), dev(sc), q8, xs, s8, out, out, M, H, H)
+    rows = list(range(0, M, 7))
+    y16, acc, bd = _rows_ref(orc, qw, sc, q8, xs, s8, rows, H, H)
+    # the GEMM epilogue: fp16(fp16(acc) + res), an fp16 add after rounding
+    ref = (y16.astype(np.float16) + R[rows]).astype(np.float16)
+    ex = acc + R[rows].astype(np.float64)
+    assert_fp16_close(host(out)[rows], ex, bd + ulp16(acc) * 2.0 ** 20, ref, what="gemm_w4a8 residual")
+    # QKV: three matrices, ragged boundaries handled per column
+    dims = (1536, 256, 256)
+    mats = [orc.synth_w4(92 + i, n, H) for i, n in enumerate(dims)]
+    outs = [empty((M, n), torch.float16) for n in dims]
+    dw = [(dev(w), dev(s)) for w, s in mats]
+    view = qe.make_qkv_view(dw[0][0], dw[0][1], outs[0], dw[1][0], dw[1][1], outs[1], dw[2][0], dw[2][1], outs[2])
+    qe.launch_gemm_prefill_qkv_w4a8(view, q8, xs, s8, M)
+    for (w, s), o, n in zip(mats, outs, dims):
+        ref, ex, bd = _rows_ref(orc, w, s, q8, xs, s8, rows, n, H)
+        assert_fp16_close(host(o)[rows], ex, bd, ref, what="gemm_w4a8 qkv")
+    # gate/up SwiGLU
+    qgu, sgu = orc.synth_w4(95, 2 * I, H)
+    mlp = empty((M, I), torch.float16)
+    qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a8(dev(qgu), dev(sgu), q8, xs, s8, mlp, M, hidden_size=H,
+                                                    intermediate_size=I)
+    hq, hx, hs = host(q8).reshape(M, H), host(xs).reshape(M, -1), host(s8).reshape(M, -1)
+    for m in rows:
+        ref, ex, bd = orc.gemv_swiglu_w4a8(qgu, sgu, hq[m], hx[m], hs[m], H, I)
+        assert_fp16_close(host(mlp)[m], ex, bd, ref, what="gemm_w4a8 swiglu")
