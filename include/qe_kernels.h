@@ -263,6 +263,30 @@ int qe_launch_attention_gqa_flash_decode_combine(const float* splitk_partial_out
                                                  uint16_t* attn_out, hipStream_t stream, int num_q_heads,
                                                  int8_t* out_q8, float* out_scale, int32_t* out_sum8);
 
+/* Stage 1 of the flash decode alone: the 16 split partials of every q head
+ * ([head][16][128] unnormalized outputs, [head][16][2] (max, denominator)),
+ * src/kernels/attention_gqa.cu:20-228.  No separate entry point in the
+ * reference API (its flash_decode launches stage 1 and stage 2 together);
+ * it feeds qe_launch_attention_combine_gemv_o_w4a8. */
+int qe_launch_attention_gqa_flash_decode_partials(const uint16_t* q, const uint16_t* layer_k_cache,
+                                                  const uint16_t* layer_v_cache, float* splitk_partial_out,
+                                                  float* splitk_partial_lse, const qe_device_control_block* d_control,
+                                                  hipStream_t stream, int num_q_heads, int num_kv_heads, int head_dim,
+                                                  int max_seq_len);
+
+/* Flash-decode stage 2 + Q8_1 epilogue (src/kernels/attention_gqa.cu:230-310)
+ * folded into the O projection's W4A8 GEMV (launch_gemv_w4a8 with residual,
+ * include/kernels.cuh:88-97): y = fp16(W_o . Q8_1(combine(partials)) +
+ * residual) in one launch, bit-identical to qe_launch_attention_gqa_flash_decode
+ * followed by qe_launch_gemv_w4a8.  attn_out_opt (16-byte aligned) receives
+ * the fp16 attention output when not NULL.  head_dim 128, at most 16 q heads,
+ * out_features rows.  No counterpart in the reference (a fusion of two of
+ * its launches). */
+int qe_launch_attention_combine_gemv_o_w4a8(const float* splitk_partial_out, const float* splitk_partial_lse,
+                                            const uint32_t* o_qweight, const uint16_t* o_scales,
+                                            const uint16_t* residual, uint16_t* output_y, uint16_t* attn_out_opt,
+                                            int out_features, int num_q_heads, int head_dim, hipStream_t stream);
+
 /* Replaces launch_attention_gqa_prefill, include/kernels.cuh:195-207. */
 int qe_launch_attention_gqa_prefill(const uint16_t* q, const uint16_t* layer_k_cache, const uint16_t* layer_v_cache,
                                     uint16_t* attn_out, const qe_device_control_block* d_control, int num_tokens,

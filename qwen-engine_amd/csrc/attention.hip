@@ -9,12 +9,13 @@
 // [kv_head][max_seq][head_dim] fp16 per layer; q [T][q_dim], k/v [T][kv_dim].
 // Head dim 128: one wave64 covers a head with 2 elements per lane, dot
 // products reduce with DPP/swizzle (seg_sum<64>).
+#include "attn_common.hpp"
 #include "rope_common.hpp"
 
 namespace qe {
 namespace {
 
-constexpr int kSplits = 16;   // FLASH_DECODE_SPLITS, include/config.cuh:29
+constexpr int kSplits = kFlashSplits;
 constexpr int kHeadDim = 128;
 constexpr int kVocab = 151936;  // VOCAB_SIZE: out-of-range token ids map to 0
 
@@ -292,34 +293,18 @@ __global__ __launch_bounds__(128) void flash_decode_stage2_kernel(const float* _
         ds[s] = ml.y;
         os[s] = part_o[row * kHeadDim + tid];
     }
-    float mg = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < kSplits; ++s)
-        if (ds[s] > 0.0f) mg = fmaxf(mg, ms[s]);
-    constexpr float kLog2e = 1.4426950408889634f;
-    float es[kSplits];  // exp(m_s - m), hardware exp2
-    float dg = 0.0f;
-#pragma unroll
-    for (int s = 0; s < kSplits; ++s) {
-        es[s] = ds[s] > 0.0f ? __builtin_amdgcn_exp2f((ms[s] - mg) * kLog2e) : 0.0f;
-        dg += ds[s] * es[s];
-    }
-    float acc = 0.0f;
-    if (dg > 0.0f) {
-        const float inv = 1.0f / dg;
-#pragma unroll
-        for (int s = 0; s < kSplits; ++s) acc += ds[s] > 0.0f ? es[s] * inv * os[s] : 0.0f;  // empty splits hold no partials
-    }
+    float wt[kSplits];
+    flash_split_weights(ms, ds, wt);
+    const float acc = flash_combine(ds, wt, os);
     attn_out[static_cast<size_t>(qh) * kHeadDim + tid] = f2h(acc);
     if (q8 == nullptr) return;  // uniform across the block
     __shared__ float s_wmax[2];
     float mx = qwen::seg_max<64>(fabsf(acc));
     if ((tid & 63) == 0) s_wmax[tid >> 6] = mx;
     __syncthreads();
-    const float d = fmaxf(fmaxf(s_wmax[0], s_wmax[1]) / 127.0f, 1e-8f);
+    const float d = flash_q8_scale(fmaxf(s_wmax[0], s_wmax[1]));
     if (tid == 0 && q_scale != nullptr) q_scale[qh] = d;
-    int v = static_cast<int>(rintf(acc / d));
-    v = max(-127, min(127, v));
+    const int v = flash_q8_value(acc, d);
     q8[static_cast<size_t>(qh) * kHeadDim + tid] = static_cast<int8_t>(v);
     int s8 = -8 * v;
     s8 += qwen::dpp_i32<0xB1>(s8);
@@ -443,6 +428,26 @@ extern "C" int qe_launch_qkv_bias_rope_kv_append(uint16_t* q, uint16_t* k, uint1
     return check_launch("qkv_bias_rope_kv_append");
 }
 
+namespace qe {
+namespace {
+int launch_flash_stage1(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, float* part_o, float* part_lse,
+                        const qe_device_control_block* ctl, hipStream_t stream, int num_q_heads, int num_kv_heads,
+                        int head_dim, int max_seq_len, const char* what) {
+    QE_REQUIRE(q && kc && vc && part_o && part_lse, "%s: NULL pointer", what);
+    QE_REQUIRE(head_dim == kHeadDim, "%s: head_dim=%d (only 128 is built)", what, head_dim);
+    QE_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, "%s: %d q heads over %d kv heads", what,
+               num_q_heads, num_kv_heads);
+    const int group = num_q_heads / num_kv_heads;
+    QE_REQUIRE(group == 1 || group == 2 || group == 4 || group == 6 || group == 8,
+               "%s: %d q heads per kv head (built: 1, 2, 4, 6, 8)", what, group);
+    QE_REQUIRE(max_seq_len > 0, "%s: max_seq_len=%d", what, max_seq_len);
+    flash_decode_stage1_kernel<<<dim3(num_kv_heads, kSplits), 256, 0, stream>>>(
+        q, kc, vc, part_o, part_lse, ctl, num_q_heads, num_kv_heads, max_seq_len);
+    return QE_OK;
+}
+}  // namespace
+}  // namespace qe
+
 extern "C" int qe_launch_attention_gqa_flash_decode(const uint16_t* q, const uint16_t* layer_k_cache,
                                                     const uint16_t* layer_v_cache, float* splitk_partial_out,
                                                     float* splitk_partial_lse, uint16_t* attn_out,
@@ -450,21 +455,25 @@ extern "C" int qe_launch_attention_gqa_flash_decode(const uint16_t* q, const uin
                                                     int num_q_heads, int num_kv_heads, int head_dim,
                                                     int max_seq_len, int8_t* out_q8, float* out_scale,
                                                     int32_t* out_sum8) {
-    QE_REQUIRE(q && layer_k_cache && layer_v_cache && splitk_partial_out && splitk_partial_lse && attn_out,
-               "attention_gqa_flash_decode: NULL pointer");
-    QE_REQUIRE(head_dim == kHeadDim, "attention_gqa_flash_decode: head_dim=%d (only 128 is built)", head_dim);
-    QE_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
-               "attention_gqa_flash_decode: %d q heads over %d kv heads", num_q_heads, num_kv_heads);
-    const int group = num_q_heads / num_kv_heads;
-    QE_REQUIRE(group == 1 || group == 2 || group == 4 || group == 6 || group == 8,
-               "attention_gqa_flash_decode: %d q heads per kv head (built: 1, 2, 4, 6, 8)", group);
-    QE_REQUIRE(max_seq_len > 0, "attention_gqa_flash_decode: max_seq_len=%d", max_seq_len);
-    flash_decode_stage1_kernel<<<dim3(num_kv_heads, kSplits), 256, 0, stream>>>(
-        q, layer_k_cache, layer_v_cache, splitk_partial_out, splitk_partial_lse, d_control, num_q_heads, num_kv_heads,
-        max_seq_len);
+    QE_REQUIRE(attn_out, "attention_gqa_flash_decode: NULL pointer");
+    QE_TRY(launch_flash_stage1(q, layer_k_cache, layer_v_cache, splitk_partial_out, splitk_partial_lse, d_control,
+                               stream, num_q_heads, num_kv_heads, head_dim, max_seq_len,
+                               "attention_gqa_flash_decode"));
     flash_decode_stage2_kernel<<<num_q_heads, 128, 0, stream>>>(splitk_partial_out, splitk_partial_lse, attn_out,
                                                                  out_q8, out_scale, out_sum8);
     return check_launch("attention_gqa_flash_decode");
+}
+
+extern "C" int qe_launch_attention_gqa_flash_decode_partials(const uint16_t* q, const uint16_t* layer_k_cache,
+                                                             const uint16_t* layer_v_cache, float* splitk_partial_out,
+                                                             float* splitk_partial_lse,
+                                                             const qe_device_control_block* d_control,
+                                                             hipStream_t stream, int num_q_heads, int num_kv_heads,
+                                                             int head_dim, int max_seq_len) {
+    QE_TRY(launch_flash_stage1(q, layer_k_cache, layer_v_cache, splitk_partial_out, splitk_partial_lse, d_control,
+                               stream, num_q_heads, num_kv_heads, head_dim, max_seq_len,
+                               "attention_gqa_flash_decode_partials"));
+    return check_launch("attention_gqa_flash_decode_partials");
 }
 
 extern "C" int qe_launch_attention_gqa_flash_decode_combine(const float* splitk_partial_out,

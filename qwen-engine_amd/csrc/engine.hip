@@ -119,11 +119,6 @@ namespace {
         hipError_t e_ = (call);                                                        \
         if (e_ != hipSuccess) return fail(QE_ERR_HIP, "%s: %s", #call, hipGetErrorString(e_)); \
     } while (0)
-#define QE_TRY(call)            \
-    do {                        \
-        int rc_ = (call);       \
-        if (rc_ != QE_OK) return rc_; \
-    } while (0)
 
 size_t mat_bytes(int rows, int K) { return align256(static_cast<size_t>(rows) * K / 2) + align256(static_cast<size_t>(rows) * (K / 128) * 2); }
 
@@ -211,12 +206,21 @@ int decode_pass(qe_engine* e, Timer* t) {
                                                      c.head_dim, c.rope_theta));
             QE_TRY(mark(e, t, 2));
         }
-        QE_TRY(qe_launch_attention_gqa_flash_decode(e->dq, kc, vc, e->part_o, e->part_lse, e->attn, e->ctl, s,
-                                                    c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_seq_len,
-                                                    e->q8, e->q8_scale, e->q8_sum8));
-        QE_TRY(mark(e, t, 1));
-        QE_TRY(qe_launch_gemv_w4a8(L.o.w, L.o.s, e->q8, e->q8_scale, e->q8_sum8, e->act0, e->act0, H,
-                                   c.num_q_heads * c.head_dim, s));
+        if (c.fused_decode && c.num_q_heads * c.head_dim <= 2048) {  // split partials, then combine + O
+            QE_TRY(qe_launch_attention_gqa_flash_decode_partials(e->dq, kc, vc, e->part_o, e->part_lse, e->ctl, s,
+                                                                 c.num_q_heads, c.num_kv_heads, c.head_dim,
+                                                                 c.max_seq_len));
+            QE_TRY(mark(e, t, 1));
+            QE_TRY(qe_launch_attention_combine_gemv_o_w4a8(e->part_o, e->part_lse, L.o.w, L.o.s, e->act0, e->act0,
+                                                           nullptr, H, c.num_q_heads, c.head_dim, s));
+        } else {
+            QE_TRY(qe_launch_attention_gqa_flash_decode(e->dq, kc, vc, e->part_o, e->part_lse, e->attn, e->ctl, s,
+                                                        c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_seq_len,
+                                                        e->q8, e->q8_scale, e->q8_sum8));
+            QE_TRY(mark(e, t, 1));
+            QE_TRY(qe_launch_gemv_w4a8(L.o.w, L.o.s, e->q8, e->q8_scale, e->q8_sum8, e->act0, e->act0, H,
+                                       c.num_q_heads * c.head_dim, s));
+        }
         if (c.fused_decode) {
             QE_TRY(qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(e->act0, L.ln2, nullptr, L.gate_up.w, L.gate_up.s,
                                                                     e->mlp, H, I, s));

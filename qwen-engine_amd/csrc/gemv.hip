@@ -26,6 +26,7 @@
 //     persistent blocks (grid capped per CU).
 // Shapes outside the fast kernel (weights not 16-byte aligned, K > 16384)
 // use a generic wave-per-row kernel that stages Q8_1 in LDS.
+#include "attn_common.hpp"
 #include "rope_common.hpp"
 #include "sample_common.hpp"
 
@@ -40,6 +41,7 @@ constexpr int kSample = 3;  // LM head: plain rows, logits optional, (value, ind
 constexpr int kXQ8 = 0;   // Q8_1 activation
 constexpr int kXF16 = 1;  // fp16 activation, quantized in the block
 constexpr int kXRMS = 2;  // fp16 activation, RMSNorm then quantized in the block
+constexpr int kXATTN = 3; // flash-decode split partials, combined and quantized in the block
 
 constexpr float kRmsEps = 1e-6f;  // RMS_NORM_EPS, include/config.cuh:20
 
@@ -54,7 +56,10 @@ struct GemvParams {
     const int32_t* s8;
     const uint16_t* x16;    // fp16 activation (kXF16 / kXRMS)
     const uint16_t* gamma;  // RMSNorm weight (kXRMS)
-    uint16_t* norm_out;     // optional fp16 normalized activation (kXRMS, block 0 writes)
+    uint16_t* norm_out;     // optional fp16 copy of the staged activation (kXRMS: normalized,
+                            // kXATTN: combined attention output; block 0 writes)
+    const float* part_o;    // kXATTN: split partials [head][16][128]
+    const float* part_lse;  // kXATTN: (max, denominator) [head][16][2]
     float* s_val;           // kSample: per-block best value / index
     int32_t* s_idx;
     const qe_device_control_block* ctl;  // kSample: temperature, rng_seed, seq_pos; QKV rope: seq_pos
@@ -312,6 +317,81 @@ __device__ __forceinline__ void stage_finish_f16(const GemvParams& p, uint4 (&ra
     }
 }
 
+// Flash-decode combine staged by the whole block (K = heads * 128): thread
+// t < K/8 owns elements 8t..8t+7 of head t/16, so a head is one 16-lane DPP
+// row.  stage_issue_attn requests that head's 16 (max, denominator) pairs and
+// the thread's 8 partial values of every split; stage_finish_attn merges them
+// (flash_split_weights / flash_combine, as the stand-alone combine kernel)
+// and quantizes with the attention epilogue's Q8_1 (rint, one group per head).
+template <int BT>
+__device__ __forceinline__ void stage_issue_attn(const GemvParams& p, float4 (&po)[kFlashSplits][2],
+                                                 float4 (&pl)[kFlashSplits / 2]) {
+    const int u = min(static_cast<int>(threadIdx.x), (p.K >> 3) - 1);
+    const int h = u >> 4, d0 = 8 * (u & 15);
+    const float* lse = p.part_lse + static_cast<size_t>(h) * kFlashSplits * 2;
+#pragma unroll
+    for (int i = 0; i < kFlashSplits / 2; ++i) pl[i] = *reinterpret_cast<const float4*>(lse + 4 * i);
+#pragma unroll
+    for (int s = 0; s < kFlashSplits; ++s) {
+        const float* o = p.part_o + (static_cast<size_t>(h) * kFlashSplits + s) * 128 + d0;
+        po[s][0] = *reinterpret_cast<const float4*>(o);
+        po[s][1] = *reinterpret_cast<const float4*>(o + 4);
+    }
+}
+
+template <int BT>
+__device__ __forceinline__ void stage_finish_attn(const GemvParams& p, const float4 (&po)[kFlashSplits][2],
+                                                  const float4 (&pl)[kFlashSplits / 2], int8_t* s_q8, int2* s_rec) {
+    const int U = p.K >> 3, KC = p.K >> 5;
+    const int u = threadIdx.x;
+    const bool ok = u < U;
+    float ms[kFlashSplits], ds[kFlashSplits], wt[kFlashSplits];
+#pragma unroll
+    for (int i = 0; i < kFlashSplits / 2; ++i) {
+        ms[2 * i] = pl[i].x;
+        ds[2 * i] = pl[i].y;
+        ms[2 * i + 1] = pl[i].z;
+        ds[2 * i + 1] = pl[i].w;
+    }
+    flash_split_weights(ms, ds, wt);
+    float acc[8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        float os[kFlashSplits];
+#pragma unroll
+        for (int s = 0; s < kFlashSplits; ++s) {
+            const float4 v = po[s][e >> 2];
+            os[s] = (e & 3) == 0 ? v.x : ((e & 3) == 1 ? v.y : ((e & 3) == 2 ? v.z : v.w));
+        }
+        acc[e] = flash_combine(ds, wt, os);
+        mx = fmaxf(mx, fabsf(acc[e]));
+    }
+    if (p.norm_out != nullptr && blockIdx.x == 0 && ok) {
+        uint32_t hw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            hw[j] = static_cast<uint32_t>(f2h(acc[2 * j])) | (static_cast<uint32_t>(f2h(acc[2 * j + 1])) << 16);
+        *reinterpret_cast<uint4*>(p.norm_out + 8 * u) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    }
+    const float d = flash_q8_scale(qwen::seg_max<16>(mx));
+    uint32_t b[8];
+    int qsum = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int v = flash_q8_value(acc[e], d);
+        qsum += v;
+        b[e] = static_cast<uint32_t>(v) & 0xFFu;
+    }
+    int8_t* dq = ok ? s_q8 + 8 * u : reinterpret_cast<int8_t*>(s_rec + KC);
+    *reinterpret_cast<int2*>(dq) = make_int2(static_cast<int>(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24)),
+                                             static_cast<int>(b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24)));
+    int csum = -8 * qsum;  // chunk = the 4 units of a DPP quad
+    csum += qwen::dpp_i32<0xB1>(csum);
+    csum += qwen::dpp_i32<0x4E>(csum);
+    s_rec[(ok && (u & 3) == 0) ? (u >> 2) : KC] = make_int2(csum, __builtin_bit_cast(int, d));
+}
+
 // QKV with RoPE: set s of block group g = s / 16 covers head g / 8; its 16
 // segments take rows j*8 + t and 64 + j*8 + t (j = g % 8, t < 8) of that head
 __device__ __forceinline__ int rope_row(int set) {
@@ -344,11 +424,15 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
     int4 xa[NCH], xb[NCH];
     int32_t xsum[NCH];
     float xd[NCH];
-    uint4 raw[XM == kXQ8 ? 1 : MAXP], graw[XM == kXQ8 ? 1 : MAXP];
+    constexpr bool XF16 = XM == kXF16 || XM == kXRMS;
+    uint4 raw[XF16 ? MAXP : 1], graw[XF16 ? MAXP : 1];
     u32x4 qa[XM == kXQ8 ? MQ : 1], qb[XM == kXQ8 ? MQ : 1];
     int4 qs4[XM == kXQ8 ? MQ : 1];
     float qxd[XM == kXQ8 ? MQ : 1];
+    constexpr int AS = XM == kXATTN ? kFlashSplits : 1;
+    float4 apo[AS][2], apl[XM == kXATTN ? kFlashSplits / 2 : 1];
     if constexpr (XM == kXQ8) stage_issue_q8<BT, MQ>(p, qa, qb, qs4, qxd);
+    else if constexpr (XM == kXATTN) stage_issue_attn<BT>(p, apo, apl);
     else stage_issue_f16<XM, BT, MAXP>(p, raw, graw);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
 
@@ -386,6 +470,7 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
         int8_t* s_q8 = reinterpret_cast<int8_t*>(s_mem);
         int2* s_rec = reinterpret_cast<int2*>(s_mem + K);
         if constexpr (XM == kXQ8) stage_finish_q8<BT, MQ>(p, qa, qb, qs4, qxd, s_q8, s_rec);
+        else if constexpr (XM == kXATTN) stage_finish_attn<BT>(p, apo, apl, s_q8, s_rec);
         else stage_finish_f16<XM, BT, MAXP>(p, raw, graw, s_q8, s_rec, s_red);
         __syncthreads();
 #pragma unroll
@@ -870,6 +955,54 @@ extern "C" int qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(const uint16_t* 
     p.n_rows = 2 * intermediate_size;
     p.K = hidden_size;
     return launch_gemv<kSwiglu, kXRMS>(p, aligned(gate_up_qweight, 16) && act_fast_ok(p), stream, what);
+}
+
+// ---- flash-decode combine folded into the O projection ------------------------------
+namespace qe {
+namespace {
+constexpr int kMaxAttnK = 2048;  // one 8-element unit per thread of a 256-thread block
+
+int launch_attn_o(const GemvParams& p, hipStream_t s) {
+    const Plan pl = plan_for(p.K, p.n_rows, kPlain, true);
+    if (pl.lpr != 16 || pl.bt != 256 || pl.rps != 1) return 0;
+    switch (pl.nch) {
+        case 2: return launch_fast<kPlain, kXATTN, 256, 16, 2, 1>(p, s);
+        case 3: return launch_fast<kPlain, kXATTN, 256, 16, 3, 1>(p, s);
+        case 6: return launch_fast<kPlain, kXATTN, 256, 16, 6, 1>(p, s);
+    }
+    return 0;
+}
+}  // namespace
+}  // namespace qe
+
+extern "C" int qe_launch_attention_combine_gemv_o_w4a8(const float* splitk_partial_out,
+                                                       const float* splitk_partial_lse, const uint32_t* o_qweight,
+                                                       const uint16_t* o_scales, const uint16_t* residual,
+                                                       uint16_t* output_y, uint16_t* attn_out_opt, int out_features,
+                                                       int num_q_heads, int head_dim, hipStream_t stream) {
+    const char* what = "attention_combine_gemv_o_w4a8";
+    QE_REQUIRE(splitk_partial_out && splitk_partial_lse && o_qweight && o_scales && output_y, "%s: NULL pointer",
+               what);
+    QE_REQUIRE(head_dim == 128, "%s: head_dim=%d (only 128 is built)", what, head_dim);
+    const int K = num_q_heads * head_dim;
+    QE_REQUIRE(num_q_heads > 0 && K <= kMaxAttnK, "%s: %d q heads (at most %d)", what, num_q_heads,
+               kMaxAttnK / 128);
+    QE_REQUIRE(out_features > 0, "%s: out_features=%d", what, out_features);
+    QE_REQUIRE(aligned(splitk_partial_out, 16) && aligned(splitk_partial_lse, 16) && aligned(o_qweight, 16) &&
+                   aligned(o_scales, 2) && aligned(residual, 2) && aligned(output_y, 2) && aligned(attn_out_opt, 16),
+               "%s: misaligned buffer (partials, weights and attn_out 16-byte aligned)", what);
+    GemvParams p{};
+    p.qw[0] = o_qweight;
+    p.sc[0] = o_scales;
+    p.out[0] = output_y;
+    p.residual = residual;
+    p.part_o = splitk_partial_out;
+    p.part_lse = splitk_partial_lse;
+    p.norm_out = attn_out_opt;
+    p.n_rows = out_features;
+    p.K = K;
+    if (!launch_attn_o(p, stream)) return fail(QE_ERR_UNSUPPORTED, "%s: no kernel for K=%d", what, K);
+    return check_launch(what);
 }
 
 // ---- fused LM head + sampling ------------------------------------------------------

@@ -54,6 +54,12 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 
 }  // namespace qe
 
+#define QE_TRY(call)                  \
+    do {                              \
+        const int rc_ = (call);       \
+        if (rc_ != QE_OK) return rc_; \
+    } while (0)
+
 #define QE_REQUIRE(cond, ...)                                              \
     do {                                                                   \
         if (!(cond)) return ::qe::fail(QE_ERR_INVALID_ARGUMENT, __VA_ARGS__); \

@@ -49,6 +49,8 @@ SIGNATURES = {
                                           ctypes.c_float],
     "qe_launch_attention_gqa_flash_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P],
     "qe_launch_attention_gqa_flash_decode_combine": [_P, _P, _P, _P, _I, _P, _P, _P],
+    "qe_launch_attention_gqa_flash_decode_partials": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I],
+    "qe_launch_attention_combine_gemv_o_w4a8": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "qe_launch_attention_gqa_prefill": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I],
 }
 
@@ -310,6 +312,22 @@ def launch_attention_gqa_flash_decode_combine(splitk_partial_out, splitk_partial
                                               out_q8=None, out_scale=None, out_sum8=None, stream=None):
     _call("qe_launch_attention_gqa_flash_decode_combine", _ptr(splitk_partial_out), _ptr(splitk_partial_lse),
           _ptr(attn_out), _stream(stream), num_q_heads, _ptr(out_q8), _ptr(out_scale), _ptr(out_sum8))
+
+
+def launch_attention_gqa_flash_decode_partials(q, layer_k_cache, layer_v_cache, splitk_partial_out,
+                                               splitk_partial_lse, d_control, stream=None, num_q_heads=12,
+                                               num_kv_heads=2, head_dim=128, max_seq_len=4096):
+    _call("qe_launch_attention_gqa_flash_decode_partials", _ptr(q), _ptr(layer_k_cache), _ptr(layer_v_cache),
+          _ptr(splitk_partial_out), _ptr(splitk_partial_lse), _ptr(d_control), _stream(stream), num_q_heads,
+          num_kv_heads, head_dim, max_seq_len)
+
+
+def launch_attention_combine_gemv_o_w4a8(splitk_partial_out, splitk_partial_lse, o_qweight, o_scales, residual,
+                                         output_y, attn_out=None, out_features=1536, num_q_heads=12, head_dim=128,
+                                         stream=None):
+    _call("qe_launch_attention_combine_gemv_o_w4a8", _ptr(splitk_partial_out), _ptr(splitk_partial_lse),
+          _ptr(o_qweight), _ptr(o_scales), _ptr(residual), _ptr(output_y), _ptr(attn_out), out_features,
+          num_q_heads, head_dim, _stream(stream))
 
 
 def launch_attention_gqa_prefill(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, stream=None,

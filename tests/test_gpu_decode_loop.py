@@ -6,6 +6,8 @@ engine built on it.
 * flash-decode combine + Q8_1 epilogue (attention_gqa.cu:263-310): bit-exact
   against the oracle when the combined value is exactly the partial (one
   active split with denominator 1);
+* combine folded into the O projection: bit-identical to the stand-alone
+  combine followed by the W4A8 GEMV (same arithmetic, one launch);
 * RoPE / flash decode / prefill attention: float kernels, checked against a
   numpy float64 statement of the same math with a stated tolerance;
 * engine: graph replay and eager launches produce the same tokens
@@ -115,6 +117,50 @@ def test_flash_decode_attention(qe, orc, seq_pos):
     qq = host(q8).astype(np.float64).reshape(nq, D)
     assert np.all(np.abs(qq * d[:, None] - got) <= d[:, None] * 0.5 + 1e-3 * np.abs(got) + 1e-6)
     assert np.array_equal(host(s8), -8 * host(q8).astype(np.int32).reshape(-1, 8).sum(1))
+
+
+@pytest.mark.parametrize("nq,nkv,seq_pos,res", [(12, 2, 0, True), (12, 2, 300, True), (12, 2, 4095, False),
+                                                 (16, 2, 77, True), (8, 1, 1000, False), (4, 4, 17, True)])
+def test_attention_combine_gemv_o_bit_identical(qe, orc, nq, nkv, seq_pos, res):
+    """partials -> (combine + Q8_1 + O GEMV + residual) in one launch equals
+    flash_decode (stage 1 + 2) -> gemv_w4a8 bit for bit; partial buffers start
+    as NaN so empty splits are never read as numbers."""
+    D, max_seq, H = 128, 4096, 1536
+    K = nq * D
+    rng = np.random.default_rng(seq_pos + nq)
+    q = rng.standard_normal((nq, D)).astype(np.float16)
+    kc = rng.standard_normal((nkv, max_seq, D)).astype(np.float16)
+    vc = rng.standard_normal((nkv, max_seq, D)).astype(np.float16)
+    qw, sc = orc.synth_w4(seq_pos + 5, H, K)
+    residual = dev((rng.standard_normal(H)).astype(np.float16)) if res else None
+    dq, dkc, dvc, dqw, dsc, ctl = dev(q), dev(kc), dev(vc), dev(qw), dev(sc), _ctl(seq_pos)
+    nan = lambda n: torch.full((n,), float("nan"), dtype=torch.float32, device="cuda")
+    part, lse = nan(nq * 16 * D), nan(nq * 16 * 2)
+    out, q8 = empty(K, torch.float16), empty(K, torch.int8)
+    xs, s8 = empty(nq, torch.float32), empty(K // 8, torch.int32)
+    qe.launch_attention_gqa_flash_decode(dq, dkc, dvc, part, lse, out, ctl, num_q_heads=nq, num_kv_heads=nkv,
+                                         head_dim=D, max_seq_len=max_seq, out_q8=q8, out_scale=xs, out_sum8=s8)
+    ref_y = empty(H, torch.float16)
+    qe.launch_gemv_w4a8(dqw, dsc, q8, xs, s8, residual, ref_y, H, K)
+    part2, lse2 = nan(nq * 16 * D), nan(nq * 16 * 2)
+    qe.launch_attention_gqa_flash_decode_partials(dq, dkc, dvc, part2, lse2, ctl, num_q_heads=nq, num_kv_heads=nkv,
+                                                  head_dim=D, max_seq_len=max_seq)
+    lse_h, lse2_h = host(lse), host(lse2)
+    assert np.array_equal(lse_h.view(np.uint32), lse2_h.view(np.uint32))
+    live = (lse_h.reshape(nq, 16, 2)[:, :, 1] > 0)
+    assert np.array_equal(host(part).reshape(nq, 16, D)[live].view(np.uint32),
+                          host(part2).reshape(nq, 16, D)[live].view(np.uint32))
+    y, attn = empty(H, torch.float16), empty(K, torch.float16)
+    qe.launch_attention_combine_gemv_o_w4a8(part2, lse2, dqw, dsc, residual, y, attn, out_features=H, num_q_heads=nq,
+                                            head_dim=D)
+    assert np.array_equal(host(attn).view(np.uint16), host(out).view(np.uint16))
+    assert np.array_equal(host(y).view(np.uint16), host(ref_y).view(np.uint16))
+    # without the attention copy, in place on the residual (the engine's call)
+    if res:
+        r2 = residual.clone()
+        qe.launch_attention_combine_gemv_o_w4a8(part2, lse2, dqw, dsc, r2, r2, None, out_features=H, num_q_heads=nq,
+                                                head_dim=D)
+        assert np.array_equal(host(r2).view(np.uint16), host(ref_y).view(np.uint16))
 
 
 def test_qkv_bias_rope_kv_append(qe):
