@@ -279,13 +279,17 @@ int qe_launch_attention_gqa_flash_decode_partials(const uint16_t* q, const uint1
  * include/kernels.cuh:88-97): y = fp16(W_o . Q8_1(combine(partials)) +
  * residual) in one launch, bit-identical to qe_launch_attention_gqa_flash_decode
  * followed by qe_launch_gemv_w4a8.  attn_out_opt (16-byte aligned) receives
- * the fp16 attention output when not NULL.  head_dim 128, at most 16 q heads,
+ * the fp16 attention output when not NULL.  d_control (seq_pos) and
+ * max_seq_len tell which splits hold positions: only the first 4, 8 or 16
+ * splits' partials are read, the fewest that cover them (all 16 when
+ * d_control is NULL).  head_dim 128, at most 16 q heads,
  * out_features rows.  No counterpart in the reference (a fusion of two of
  * its launches). */
 int qe_launch_attention_combine_gemv_o_w4a8(const float* splitk_partial_out, const float* splitk_partial_lse,
                                             const uint32_t* o_qweight, const uint16_t* o_scales,
                                             const uint16_t* residual, uint16_t* output_y, uint16_t* attn_out_opt,
-                                            int out_features, int num_q_heads, int head_dim, hipStream_t stream);
+                                            const qe_device_control_block* d_control, int out_features,
+                                            int num_q_heads, int head_dim, int max_seq_len, hipStream_t stream);
 
 /* Replaces launch_attention_gqa_prefill, include/kernels.cuh:195-207. */
 int qe_launch_attention_gqa_prefill(const uint16_t* q, const uint16_t* layer_k_cache, const uint16_t* layer_v_cache,

@@ -105,171 +105,251 @@ __global__ __launch_bounds__(256) void qkv_bias_rope_kv_append_kernel(
 }
 
 // ---- flash decode, stage 1 -----------------------------------------------------
-// grid (num_kv_heads, kSplits), 256 threads.  A split is a contiguous run
-// of at most 256 positions.  Each wave takes 4 positions per step, one per
-// 16-lane group; lane j of a group holds dims 8j..8j+7 (one 16-byte K and V
-// load per position), so a score is a 16-lane DPP sum.  K and V rows of
-// four steps (64 positions per block) are requested before any of them is
-// used.  Online softmax per lane group in the exp2 domain; the 4 groups and
-// 4 waves are merged at the end.  Output per (q head, split): unnormalized
-// o relative to the split max m, and (m, denominator) with m in natural-log
-// units, as attention_gqa.cu's stage 1 writes them.
-constexpr int kRound = 4;  // wave steps per round of loads
+// grid (num_q_heads / GH, kSplits), NT = 512 threads; a block takes GH = half
+// of the q heads of one kv head (two blocks per kv head, so each wave has
+// half the per-position arithmetic).  A split is a contiguous run of
+// flash_split_len(seq_len) positions (the reference's ceil(seq_len / 16), at
+// least kFlashMinSplit).  The NT/16 lane groups of the block (16 lanes each)
+// each take one position per step; lane j of a group holds dims 8j..8j+7 (one
+// 16-byte K and V load per position), so a score is a v_dot2 chain plus a
+// 16-lane DPP sum.  A round is 64 positions whose K and V rows are requested
+// together; with more than one round the next round's rows are requested
+// before the current one is used.  Softmax state per lane group in the exp2
+// domain, rescaled once per round.  The lane-group states are merged through
+// LDS (max, weights, weighted sum), up to 48 KB of partial outputs per pass.
+// Output per (q head, split): unnormalized o relative to the split max m, and
+// (m, denominator) with m in natural-log units, as attention_gqa.cu's stage 1
+// writes them.
+//
+// QE_S1_TIMING=1 builds a timing probe: block-level timestamps of each phase
+// (s_memrealtime, 100 MHz) into g_dbg_ts, read back with qe_debug_ts.
+#ifndef QE_FLASH_NT
+#define QE_FLASH_NT 512
+#endif
+#if QE_S1_TIMING
+__device__ unsigned long long g_dbg_ts[256][8];
+#define QE_TS(i, wait)                                                                                  \
+    do {                                                                                                \
+        if (wait) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");                          \
+        __builtin_amdgcn_sched_barrier(0);                                                              \
+        const unsigned long long t_ = __builtin_amdgcn_s_memrealtime();                                 \
+        if (threadIdx.x == 0) g_dbg_ts[blockIdx.y * gridDim.x + blockIdx.x][i] = t_;                     \
+        __builtin_amdgcn_sched_barrier(0);                                                              \
+    } while (0)
+#define QE_TS_ZERO(i) \
+    if (threadIdx.x == 0) g_dbg_ts[blockIdx.y * gridDim.x + blockIdx.x][i] = 0
+#else
+#define QE_TS_ZERO(i)
+#define QE_TS(i, wait) \
+    do {               \
+    } while (0)
+#endif
 
-__device__ __forceinline__ void unpack8_f32(const u32x4 w, float (&f)[8]) {
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+template <int GH>
+struct FlashState {
+    float m[GH], l[GH], o[GH][8];
+};
+
+// One round: step st < kSteps at positions r0 + NG*st + gid (NG lane groups).
+template <int GH, int NG>
+__device__ __forceinline__ void flash_round(FlashState<GH>& S, const u32x4 (&qraw)[GH], const u32x4 (&kr)[64 / NG],
+                                            const u32x4 (&vr)[64 / NG], int r0, int t1, int gid) {
+    constexpr int kSteps = 64 / NG;
+    constexpr float kScale = 1.4426950408889634f * 0.08838834764831845f;  // log2(e) / sqrt(128)
+    const int steps = min(kSteps, (t1 - r0 + NG - 1) / NG);
+    float sc[GH][kSteps];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f[2 * i] = h2f(static_cast<uint16_t>(w[i] & 0xFFFFu));
-        f[2 * i + 1] = h2f(static_cast<uint16_t>(w[i] >> 16));
+    for (int st = 0; st < kSteps; ++st) {
+        const bool valid = st < steps && r0 + st * NG + gid < t1;
+#pragma unroll
+        for (int h = 0; h < GH; ++h) {
+            float d = 0.0f;
+            if (st < steps) {  // block-uniform
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // copy the vector element first: a bit_cast straight from an
+                    // element of an ext_vector always read element 0 (clang 22)
+                    const uint32_t qw = qraw[h][i], kw = kr[st][i];
+                    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, qw), __builtin_bit_cast(f16x2, kw), d, false);
+                }
+                d = qwen::seg_sum<16>(d) * kScale;
+            }
+            sc[h][st] = valid ? d : -INFINITY;
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < GH; ++h) {
+        float mn = S.m[h];
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) mn = fmaxf(mn, sc[h][st]);
+        // no valid position yet: keep everything at zero
+        const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(S.m[h] - mn);
+        float l = S.l[h] * alpha;
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = S.o[h][i] * alpha;
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+            if (st < steps) {
+                const float p = sc[h][st] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[h][st] - mn);
+                l += p;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t vw = vr[st][i];
+                    const f16x2 v2 = __builtin_bit_cast(f16x2, vw);
+                    o[2 * i] += p * static_cast<float>(v2.x);
+                    o[2 * i + 1] += p * static_cast<float>(v2.y);
+                }
+            }
+        }
+        S.m[h] = mn;
+        S.l[h] = l;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) S.o[h][i] = o[i];
     }
 }
 
-template <int GROUP>
+// One block: GH q heads (qh0..qh0+GH-1) of kv head kvh over positions [t0, t1)
+// with NT threads (NT/16 lane groups).
+template <int GH, int NT>
 __device__ __forceinline__ void flash_decode_split(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
                                                    const uint16_t* __restrict__ vc, float* __restrict__ part_o,
-                                                   float* __restrict__ part_lse, int kvh, int split, int t0, int t1,
-                                                   int max_seq) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int g = lane >> 4, j = lane & 15;
-    const int qh0 = kvh * GROUP;
-    constexpr float kLog2e = 1.4426950408889634f;
-    const float sc2 = kLog2e / sqrtf(static_cast<float>(kHeadDim));  // scores scaled into the exp2 domain
-    float qf[GROUP][8];
-#pragma unroll
-    for (int h = 0; h < GROUP; ++h) {
-        float f[8];
-        unpack8_f32(*reinterpret_cast<const u32x4*>(q + (qh0 + h) * kHeadDim + 8 * j), f);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) qf[h][i] = f[i] * sc2;
-    }
-    float mh[GROUP], lh[GROUP], oh[GROUP][8];
-#pragma unroll
-    for (int h = 0; h < GROUP; ++h) {
-        mh[h] = -INFINITY;
-        lh[h] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) oh[h][i] = 0.0f;
-    }
+                                                   float* __restrict__ part_lse, int kvh, int qh0, int split, int t0,
+                                                   int t1, int max_seq) {
+    constexpr int NG = NT / 16, kSteps = 64 / NG;
+    const int gid = threadIdx.x >> 4, j = threadIdx.x & 15;  // lane group of the block, lane in the group
     const size_t base = static_cast<size_t>(kvh) * max_seq * kHeadDim + 8 * j;
-    for (int r0 = t0; r0 < t1; r0 += 64) {
-        u32x4 kr[kRound], vr[kRound];
+    // every load is unconditional (positions clamped to the split)
+    auto load_round = [&](int r0, u32x4 (&kr)[kSteps], u32x4 (&vr)[kSteps]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int st = 0; st < kRound; ++st) {
-            const int t = min(r0 + st * 16 + wave * 4 + g, t1 - 1);
-            kr[st] = *reinterpret_cast<const u32x4*>(kc + base + static_cast<size_t>(t) * kHeadDim);
-            vr[st] = *reinterpret_cast<const u32x4*>(vc + base + static_cast<size_t>(t) * kHeadDim);
+        for (int st = 0; st < kSteps; ++st) {
+            const int t = min(r0 + st * NG + gid, t1 - 1);
+            kr[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kc + base + static_cast<size_t>(t) * kHeadDim));
+            vr[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vc + base + static_cast<size_t>(t) * kHeadDim));
         }
-        const int steps = min(kRound, (t1 - r0 + 15) / 16);  // block-uniform: skip empty steps
+    };
+    u32x4 qraw[GH];
 #pragma unroll
-        for (int st = 0; st < kRound; ++st) {
-            if (st >= steps) break;
-            const bool valid = r0 + st * 16 + wave * 4 + g < t1;
-            float kf[8], vf[8];
-            unpack8_f32(kr[st], kf);
-            unpack8_f32(vr[st], vf);
+    for (int h = 0; h < GH; ++h) qraw[h] = *reinterpret_cast<const u32x4*>(q + (qh0 + h) * kHeadDim + 8 * j);
+    u32x4 ka[kSteps], va[kSteps];
+    load_round(t0, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+    QE_TS(2, true);
+    FlashState<GH> S;
 #pragma unroll
-            for (int h = 0; h < GROUP; ++h) {
-                float d = 0.0f;
+    for (int h = 0; h < GH; ++h) {
+        S.m[h] = -INFINITY;
+        S.l[h] = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) d += qf[h][i] * kf[i];
-                const float sc = qwen::seg_sum<16>(d);
-                const float mn = valid ? fmaxf(mh[h], sc) : mh[h];
-                const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mh[h] - mn);
-                const float p = valid ? __builtin_amdgcn_exp2f(sc - mn) : 0.0f;
-                lh[h] = lh[h] * alpha + p;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) oh[h][i] = oh[h][i] * alpha + p * vf[i];
-                mh[h] = mn;
-            }
+        for (int i = 0; i < 8; ++i) S.o[h][i] = 0.0f;
+    }
+    if (t1 - t0 <= 64) {  // one round (every split of a context up to 16 * 64 positions)
+        flash_round<GH, NG>(S, qraw, ka, va, t0, t1, gid);
+    } else {  // ping-pong: the next round's rows are in flight while this one is used
+        u32x4 kb[kSteps], vb[kSteps];
+        for (int r0 = t0;;) {
+            load_round(min(r0 + 64, t1 - 1), kb, vb);
+            __builtin_amdgcn_sched_barrier(0);
+            flash_round<GH, NG>(S, qraw, ka, va, r0, t1, gid);
+            r0 += 64;
+            if (r0 >= t1) break;
+            load_round(min(r0 + 64, t1 - 1), ka, va);
+            __builtin_amdgcn_sched_barrier(0);
+            flash_round<GH, NG>(S, qraw, kb, vb, r0, t1, gid);
+            r0 += 64;
+            if (r0 >= t1) break;
         }
     }
-    // merge the 4 lane groups of the wave (lanes j, j+16, j+32, j+48)
-#pragma unroll
-    for (int h = 0; h < GROUP; ++h) {
-#pragma unroll
-        for (int sh = 0; sh < 2; ++sh) {
-            const float mo = sh == 0 ? qwen::swz_xor16_f32(mh[h]) : __shfl_xor(mh[h], 32);
-            const float lo = sh == 0 ? qwen::swz_xor16_f32(lh[h]) : __shfl_xor(lh[h], 32);
-            const float mn = fmaxf(mh[h], mo);
-            const float a = mh[h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mh[h] - mn);
-            const float b = mo == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mn);
-            lh[h] = lh[h] * a + lo * b;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float oo = sh == 0 ? qwen::swz_xor16_f32(oh[h][i]) : __shfl_xor(oh[h][i], 32);
-                oh[h][i] = oh[h][i] * a + oo * b;
-            }
-            mh[h] = mn;
-        }
-    }
-    // merge the 4 waves through LDS; wave 0 writes
-    __shared__ float s_ml[4][GROUP][2];
-    __shared__ float s_o[4][GROUP][kHeadDim];
-    if (lane < 16) {
-#pragma unroll
-        for (int h = 0; h < GROUP; ++h) {
-            if (lane == 0) {
-                s_ml[wave][h][0] = mh[h];
-                s_ml[wave][h][1] = lh[h];
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) s_o[wave][h][8 * j + i] = oh[h][i];
-        }
-    }
-    __syncthreads();
-    // thread (h, d) for h < GROUP, d < 128: 2 elements per thread over 256 threads
+    QE_TS(3, false);
+    // merge the NG lane-group states through LDS, HP heads per pass (48 KB):
+    // M = max_g m_g, w_g = exp2(m_g - M), L = sum_g l_g w_g, o = sum_g w_g o_g
+    constexpr int HP = (GH * NG <= 96) ? GH : 96 / NG;
+    __shared__ __align__(16) float s_o[NG][HP][kHeadDim];
+    __shared__ float s_m[NG][HP], s_l[NG][HP], s_w[HP][NG];
     constexpr float kLn2 = 0.6931471805599453f;
-    for (int idx = threadIdx.x; idx < GROUP * kHeadDim; idx += 256) {
-        const int h = idx / kHeadDim, d = idx % kHeadDim;
-        float mx = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) mx = fmaxf(mx, s_ml[w][h][0]);
-        float lt = 0.0f, o = 0.0f;
+    for (int h0 = 0; h0 < GH; h0 += HP) {
+        if (h0 > 0) __syncthreads();  // the previous pass has read s_o
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float f = s_ml[w][h][0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_ml[w][h][0] - mx);
-            lt += s_ml[w][h][1] * f;
-            o += s_o[w][h][d] * f;
+        for (int hh = 0; hh < HP; ++hh) {
+            if (h0 + hh < GH) {
+                float4* dst = reinterpret_cast<float4*>(&s_o[gid][hh][8 * j]);
+                dst[0] = make_float4(S.o[h0 + hh][0], S.o[h0 + hh][1], S.o[h0 + hh][2], S.o[h0 + hh][3]);
+                dst[1] = make_float4(S.o[h0 + hh][4], S.o[h0 + hh][5], S.o[h0 + hh][6], S.o[h0 + hh][7]);
+                if (j == 0) {
+                    s_m[gid][hh] = S.m[h0 + hh];
+                    s_l[gid][hh] = S.l[h0 + hh];
+                }
+            }
         }
-        const size_t row = static_cast<size_t>(qh0 + h) * kSplits + split;
-        part_o[row * kHeadDim + d] = o;
-        if (d == 0) {
-            part_lse[row * 2] = mx * kLn2;  // natural-log units
-            part_lse[row * 2 + 1] = lt;
+        __syncthreads();
+        const int t = threadIdx.x;
+        const int nh = min(HP, GH - h0);
+        if (t < nh * NG) {  // thread (head t/NG, lane group t%NG): NG consecutive lanes per head
+            const int hh = t / NG, g = t % NG;
+            const float m = s_m[g][hh];
+            const float mx = qwen::seg_max<NG>(m);
+            const float w = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mx);
+            const float lt = qwen::seg_sum<NG>(s_l[g][hh] * w);
+            s_w[hh][g] = w;
+            if (g == 0) {
+                const size_t row = static_cast<size_t>(qh0 + h0 + hh) * kSplits + split;
+                part_lse[row * 2] = mx * kLn2;  // natural-log units (-inf with no positions; lt is 0 then)
+                part_lse[row * 2 + 1] = lt;
+            }
+        }
+        __syncthreads();
+        if (t < nh * 32) {  // thread (head t/32, dims 4*(t%32)..+3)
+            const int hh = t >> 5, d = 4 * (t & 31);
+            float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                const float w = s_w[hh][g];
+                const float4 v = *reinterpret_cast<const float4*>(&s_o[g][hh][d]);
+                o.x += w * v.x;
+                o.y += w * v.y;
+                o.z += w * v.z;
+                o.w += w * v.w;
+            }
+            const size_t row = static_cast<size_t>(qh0 + h0 + hh) * kSplits + split;
+            *reinterpret_cast<float4*>(part_o + row * kHeadDim + d) = o;
         }
     }
+    QE_TS(5, false);
+    QE_TS(6, true);
 }
 
-__global__ __launch_bounds__(256) void flash_decode_stage1_kernel(const uint16_t* __restrict__ q,
-                                                                  const uint16_t* __restrict__ kc,
-                                                                  const uint16_t* __restrict__ vc,
-                                                                  float* __restrict__ part_o,
-                                                                  float* __restrict__ part_lse,
-                                                                  const qe_device_control_block* ctl, int nq,
-                                                                  int nkv, int max_seq) {
-    const int kvh = blockIdx.x, split = blockIdx.y;
-    const int group = nq / nkv;
+// grid (num_kv_heads * group / GH, kSplits): block x covers q heads
+// GH*x .. GH*x + GH - 1 (kv head GH*x / group).
+template <int GH, int NT>
+__global__ __launch_bounds__(NT) void flash_decode_stage1_kernel(const uint16_t* __restrict__ q,
+                                                                 const uint16_t* __restrict__ kc,
+                                                                 const uint16_t* __restrict__ vc,
+                                                                 float* __restrict__ part_o,
+                                                                 float* __restrict__ part_lse,
+                                                                 const qe_device_control_block* ctl, int group,
+                                                                 int max_seq) {
+    const int qh0 = blockIdx.x * GH, split = blockIdx.y;
+    const int kvh = qh0 / group;
+    QE_TS(0, false);
     const int seq_pos = ctl != nullptr ? ctl->seq_pos : 0;
     const int seq_len = min(seq_pos + 1, max_seq);
-    const int per = (seq_len + kSplits - 1) / kSplits;
+    const int per = flash_split_len(seq_len);
     const int t0 = split * per;
     const int t1 = min(t0 + per, seq_len);
+    QE_TS(1, true);
     if (t0 >= t1) {
-        if (threadIdx.x < group) {
-            const size_t li = (static_cast<size_t>(kvh * group + threadIdx.x) * kSplits + split) * 2;
+        QE_TS_ZERO(6);
+        if (threadIdx.x < GH) {
+            const size_t li = (static_cast<size_t>(qh0 + threadIdx.x) * kSplits + split) * 2;
             part_lse[li] = -INFINITY;
             part_lse[li + 1] = 0.0f;
         }
         return;
     }
-    switch (group) {  // q heads per kv head: compile-time so every array stays in VGPRs
-        case 1: flash_decode_split<1>(q, kc, vc, part_o, part_lse, kvh, split, t0, t1, max_seq); break;
-        case 2: flash_decode_split<2>(q, kc, vc, part_o, part_lse, kvh, split, t0, t1, max_seq); break;
-        case 4: flash_decode_split<4>(q, kc, vc, part_o, part_lse, kvh, split, t0, t1, max_seq); break;
-        case 6: flash_decode_split<6>(q, kc, vc, part_o, part_lse, kvh, split, t0, t1, max_seq); break;
-        case 8: flash_decode_split<8>(q, kc, vc, part_o, part_lse, kvh, split, t0, t1, max_seq); break;
-        default: break;  // rejected on the host
-    }
+    flash_decode_split<GH, NT>(q, kc, vc, part_o, part_lse, kvh, qh0, split, t0, t1, max_seq);
 }
 
 // ---- flash decode, stage 2 + Q8_1 epilogue ---------------------------------------
@@ -441,8 +521,16 @@ int launch_flash_stage1(const uint16_t* q, const uint16_t* kc, const uint16_t* v
     QE_REQUIRE(group == 1 || group == 2 || group == 4 || group == 6 || group == 8,
                "%s: %d q heads per kv head (built: 1, 2, 4, 6, 8)", what, group);
     QE_REQUIRE(max_seq_len > 0, "%s: max_seq_len=%d", what, max_seq_len);
-    flash_decode_stage1_kernel<<<dim3(num_kv_heads, kSplits), 256, 0, stream>>>(
-        q, kc, vc, part_o, part_lse, ctl, num_q_heads, num_kv_heads, max_seq_len);
+    // q heads per block: half of a kv head's group (two blocks per kv head)
+    const dim3 grid2(num_q_heads / (group > 1 ? group / 2 : 1), kSplits);
+    constexpr int NT = QE_FLASH_NT;
+    switch (group) {
+        case 1: flash_decode_stage1_kernel<1, NT><<<grid2, NT, 0, stream>>>(q, kc, vc, part_o, part_lse, ctl, group, max_seq_len); break;
+        case 2: flash_decode_stage1_kernel<1, NT><<<grid2, NT, 0, stream>>>(q, kc, vc, part_o, part_lse, ctl, group, max_seq_len); break;
+        case 4: flash_decode_stage1_kernel<2, NT><<<grid2, NT, 0, stream>>>(q, kc, vc, part_o, part_lse, ctl, group, max_seq_len); break;
+        case 6: flash_decode_stage1_kernel<3, NT><<<grid2, NT, 0, stream>>>(q, kc, vc, part_o, part_lse, ctl, group, max_seq_len); break;
+        case 8: flash_decode_stage1_kernel<4, NT><<<grid2, NT, 0, stream>>>(q, kc, vc, part_o, part_lse, ctl, group, max_seq_len); break;
+    }
     return QE_OK;
 }
 }  // namespace
@@ -463,6 +551,12 @@ extern "C" int qe_launch_attention_gqa_flash_decode(const uint16_t* q, const uin
                                                                  out_q8, out_scale, out_sum8);
     return check_launch("attention_gqa_flash_decode");
 }
+
+#if QE_S1_TIMING
+extern "C" int qe_debug_ts(void* host) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(qe::g_dbg_ts), sizeof(qe::g_dbg_ts)) == hipSuccess ? 0 : 1;
+}
+#endif
 
 extern "C" int qe_launch_attention_gqa_flash_decode_partials(const uint16_t* q, const uint16_t* layer_k_cache,
                                                              const uint16_t* layer_v_cache, float* splitk_partial_out,

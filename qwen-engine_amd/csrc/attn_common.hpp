@@ -12,6 +12,23 @@ namespace qe {
 
 constexpr int kFlashSplits = 16;  // FLASH_DECODE_SPLITS, include/config.cuh:29
 
+// Positions per split for a context of seq_len positions: the reference's
+// ceil(seq_len / 16), but at least kFlashMinSplit, so that short contexts
+// fill fewer splits (one round of loads per block either way) and the
+// combine reads fewer partials.  Splits past the context hold no positions.
+#ifndef QE_FLASH_MIN_SPLIT
+#define QE_FLASH_MIN_SPLIT 64
+#endif
+constexpr int kFlashMinSplit = QE_FLASH_MIN_SPLIT;
+__host__ __device__ __forceinline__ int flash_split_len(int seq_len) {
+    const int per = (seq_len + kFlashSplits - 1) / kFlashSplits;
+    return per > kFlashMinSplit ? per : kFlashMinSplit;
+}
+__host__ __device__ __forceinline__ int flash_live_splits(int seq_len) {
+    const int per = flash_split_len(seq_len);
+    return (seq_len + per - 1) / per;
+}
+
 // Split weights w_s = exp(m_s - m) / sum_t d_t exp(m_t - m) over the splits
 // that hold positions (d_s > 0); m is their largest max.  With no positions
 // at all every weight is 0.  m_s is in natural-log units; exp uses exp2.
@@ -35,12 +52,28 @@ __device__ __forceinline__ void flash_split_weights(const float (&ms)[kFlashSpli
 }
 
 // One output element: sum_s w_s * o_s over the non-empty splits (the
-// partials of empty splits are never read as numbers).
+// partials of empty splits are never read as numbers).  Product and sum are
+// rounded separately (no fused multiply-add), so that skipping splits known
+// to be empty (flash_combine_live) gives the same bits: acc starts at +0 and
+// adding +0 never changes it.
 __device__ __forceinline__ float flash_combine(const float (&ds)[kFlashSplits], const float (&wt)[kFlashSplits],
                                                const float (&os)[kFlashSplits]) {
+#pragma clang fp contract(off)
     float acc = 0.0f;
 #pragma unroll
     for (int s = 0; s < kFlashSplits; ++s) acc += ds[s] > 0.0f ? wt[s] * os[s] : 0.0f;
+    return acc;
+}
+
+// The same over the first `live` splits only (block-uniform); every split
+// from `live` on holds no positions.
+__device__ __forceinline__ float flash_combine_live(const float (&ds)[kFlashSplits], const float (&wt)[kFlashSplits],
+                                                    const float (&os)[kFlashSplits], int live) {
+#pragma clang fp contract(off)
+    float acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kFlashSplits; ++s)
+        if (s < live) acc += ds[s] > 0.0f ? wt[s] * os[s] : 0.0f;
     return acc;
 }
 

@@ -212,7 +212,8 @@ int decode_pass(qe_engine* e, Timer* t) {
                                                                  c.max_seq_len));
             QE_TRY(mark(e, t, 1));
             QE_TRY(qe_launch_attention_combine_gemv_o_w4a8(e->part_o, e->part_lse, L.o.w, L.o.s, e->act0, e->act0,
-                                                           nullptr, H, c.num_q_heads, c.head_dim, s));
+                                                           nullptr, e->ctl, H, c.num_q_heads, c.head_dim,
+                                                           c.max_seq_len, s));
         } else {
             QE_TRY(qe_launch_attention_gqa_flash_decode(e->dq, kc, vc, e->part_o, e->part_lse, e->attn, e->ctl, s,
                                                         c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_seq_len,

@@ -41,7 +41,11 @@ constexpr int kSample = 3;  // LM head: plain rows, logits optional, (value, ind
 constexpr int kXQ8 = 0;   // Q8_1 activation
 constexpr int kXF16 = 1;  // fp16 activation, quantized in the block
 constexpr int kXRMS = 2;  // fp16 activation, RMSNorm then quantized in the block
-constexpr int kXATTN = 3; // flash-decode split partials, combined and quantized in the block
+// flash-decode split partials, combined and quantized in the block; the
+// first 4, 8 or all 16 splits are read
+constexpr int kXATTN4 = 3;
+constexpr int kXATTN8 = 4;
+constexpr int kXATTN16 = 5;
 
 constexpr float kRmsEps = 1e-6f;  // RMS_NORM_EPS, include/config.cuh:20
 
@@ -57,9 +61,9 @@ struct GemvParams {
     const uint16_t* x16;    // fp16 activation (kXF16 / kXRMS)
     const uint16_t* gamma;  // RMSNorm weight (kXRMS)
     uint16_t* norm_out;     // optional fp16 copy of the staged activation (kXRMS: normalized,
-                            // kXATTN: combined attention output; block 0 writes)
-    const float* part_o;    // kXATTN: split partials [head][16][128]
-    const float* part_lse;  // kXATTN: (max, denominator) [head][16][2]
+                            // attention: combined attention output; block 0 writes)
+    const float* part_o;    // attention: split partials [head][16][128]
+    const float* part_lse;  // attention: (max, denominator) [head][16][2]
     float* s_val;           // kSample: per-block best value / index
     int32_t* s_idx;
     const qe_device_control_block* ctl;  // kSample: temperature, rng_seed, seq_pos; QKV rope: seq_pos
@@ -319,35 +323,46 @@ __device__ __forceinline__ void stage_finish_f16(const GemvParams& p, uint4 (&ra
 
 // Flash-decode combine staged by the whole block (K = heads * 128): thread
 // t < K/8 owns elements 8t..8t+7 of head t/16, so a head is one 16-lane DPP
-// row.  stage_issue_attn requests that head's 16 (max, denominator) pairs and
-// the thread's 8 partial values of every split; stage_finish_attn merges them
-// (flash_split_weights / flash_combine, as the stand-alone combine kernel)
-// and quantizes with the attention epilogue's Q8_1 (rint, one group per head).
-template <int BT>
-__device__ __forceinline__ void stage_issue_attn(const GemvParams& p, float4 (&po)[kFlashSplits][2],
-                                                 float4 (&pl)[kFlashSplits / 2]) {
+// row.  The kernel body is instantiated for LS = 4, 8 or 16 loaded splits
+// and picks the smallest that covers the splits holding positions (from the
+// control block), so every load is unconditional.  stage_issue_attn requests
+// the head's (max, denominator) pairs and the thread's 8 partial values of
+// splits s < LS; stage_finish_attn merges them (flash_split_weights /
+// flash_combine: the stand-alone combine kernel's arithmetic; splits without
+// positions have denominator 0 and contribute nothing) and quantizes with the
+// attention epilogue's Q8_1 (rint, one group per head).
+constexpr int attn_splits(int XM) { return XM == kXATTN4 ? 4 : (XM == kXATTN8 ? 8 : 16); }
+constexpr bool is_attn(int XM) { return XM >= kXATTN4; }
+
+template <int LS>
+__device__ __forceinline__ void stage_issue_attn(const GemvParams& p, float4 (&po)[LS][2], float4 (&pl)[LS / 2]) {
     const int u = min(static_cast<int>(threadIdx.x), (p.K >> 3) - 1);
     const int h = u >> 4, d0 = 8 * (u & 15);
     const float* lse = p.part_lse + static_cast<size_t>(h) * kFlashSplits * 2;
 #pragma unroll
-    for (int i = 0; i < kFlashSplits / 2; ++i) pl[i] = *reinterpret_cast<const float4*>(lse + 4 * i);
+    for (int i = 0; i < LS / 2; ++i) pl[i] = *reinterpret_cast<const float4*>(lse + 4 * i);
+    const float* o = p.part_o + static_cast<size_t>(h) * kFlashSplits * 128 + d0;
 #pragma unroll
-    for (int s = 0; s < kFlashSplits; ++s) {
-        const float* o = p.part_o + (static_cast<size_t>(h) * kFlashSplits + s) * 128 + d0;
-        po[s][0] = *reinterpret_cast<const float4*>(o);
-        po[s][1] = *reinterpret_cast<const float4*>(o + 4);
+    for (int s = 0; s < LS; ++s) {
+        po[s][0] = *reinterpret_cast<const float4*>(o + s * 128);
+        po[s][1] = *reinterpret_cast<const float4*>(o + s * 128 + 4);
     }
 }
 
-template <int BT>
-__device__ __forceinline__ void stage_finish_attn(const GemvParams& p, const float4 (&po)[kFlashSplits][2],
-                                                  const float4 (&pl)[kFlashSplits / 2], int8_t* s_q8, int2* s_rec) {
+template <int LS>
+__device__ __forceinline__ void stage_finish_attn(const GemvParams& p, const float4 (&po)[LS][2],
+                                                  const float4 (&pl)[LS / 2], int8_t* s_q8, int2* s_rec) {
     const int U = p.K >> 3, KC = p.K >> 5;
     const int u = threadIdx.x;
     const bool ok = u < U;
     float ms[kFlashSplits], ds[kFlashSplits], wt[kFlashSplits];
 #pragma unroll
-    for (int i = 0; i < kFlashSplits / 2; ++i) {
+    for (int s = 0; s < kFlashSplits; ++s) {
+        ms[s] = -INFINITY;
+        ds[s] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < LS / 2; ++i) {
         ms[2 * i] = pl[i].x;
         ds[2 * i] = pl[i].y;
         ms[2 * i + 1] = pl[i].z;
@@ -361,8 +376,12 @@ __device__ __forceinline__ void stage_finish_attn(const GemvParams& p, const flo
         float os[kFlashSplits];
 #pragma unroll
         for (int s = 0; s < kFlashSplits; ++s) {
-            const float4 v = po[s][e >> 2];
-            os[s] = (e & 3) == 0 ? v.x : ((e & 3) == 1 ? v.y : ((e & 3) == 2 ? v.z : v.w));
+            if (s < LS) {
+                const float4 v = po[s][e >> 2];
+                os[s] = (e & 3) == 0 ? v.x : ((e & 3) == 1 ? v.y : ((e & 3) == 2 ? v.z : v.w));
+            } else {
+                os[s] = 0.0f;
+            }
         }
         acc[e] = flash_combine(ds, wt, os);
         mx = fmaxf(mx, fabsf(acc[e]));
@@ -401,7 +420,7 @@ __device__ __forceinline__ int rope_row(int set) {
 }
 
 template <int BT, int LPR, int NCH, int RPS, int MODE, int XM, bool LOOP>
-__global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
+__device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
     // SwiGLU: a segment owns a (gate, up) row pair (RPS 2), or, with 16-lane
     // segments and RPS 1, segments 2s and 2s+1 own the gate and up row and
     // meet through a 32-lane swizzle
@@ -429,10 +448,10 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
     u32x4 qa[XM == kXQ8 ? MQ : 1], qb[XM == kXQ8 ? MQ : 1];
     int4 qs4[XM == kXQ8 ? MQ : 1];
     float qxd[XM == kXQ8 ? MQ : 1];
-    constexpr int AS = XM == kXATTN ? kFlashSplits : 1;
-    float4 apo[AS][2], apl[XM == kXATTN ? kFlashSplits / 2 : 1];
+    constexpr int LS = attn_splits(XM);
+    float4 apo[is_attn(XM) ? LS : 1][2], apl[is_attn(XM) ? LS / 2 : 1];
     if constexpr (XM == kXQ8) stage_issue_q8<BT, MQ>(p, qa, qb, qs4, qxd);
-    else if constexpr (XM == kXATTN) stage_issue_attn<BT>(p, apo, apl);
+    else if constexpr (is_attn(XM)) stage_issue_attn<LS>(p, apo, apl);
     else stage_issue_f16<XM, BT, MAXP>(p, raw, graw);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
 
@@ -470,7 +489,7 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
         int8_t* s_q8 = reinterpret_cast<int8_t*>(s_mem);
         int2* s_rec = reinterpret_cast<int2*>(s_mem + K);
         if constexpr (XM == kXQ8) stage_finish_q8<BT, MQ>(p, qa, qb, qs4, qxd, s_q8, s_rec);
-        else if constexpr (XM == kXATTN) stage_finish_attn<BT>(p, apo, apl, s_q8, s_rec);
+        else if constexpr (is_attn(XM)) stage_finish_attn<LS>(p, apo, apl, s_q8, s_rec);
         else stage_finish_f16<XM, BT, MAXP>(p, raw, graw, s_q8, s_rec, s_red);
         __syncthreads();
 #pragma unroll
@@ -608,6 +627,30 @@ __global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams p) {
             p.s_idx[blockIdx.x] = b.i;
         }
     }
+}
+
+// The kernels read the parameter block in place (the kernel-argument
+// segment, scalar loads): binding the by-value parameter to a reference would
+// make the compiler copy it to private memory.
+__device__ __forceinline__ const GemvParams& kernel_params() {
+    return *(const GemvParams*)__builtin_amdgcn_kernarg_segment_ptr();  // C cast: drops the address space
+}
+
+template <int BT, int LPR, int NCH, int RPS, int MODE, int XM, bool LOOP>
+__global__ __launch_bounds__(BT) void gemv_w4_kernel(GemvParams) {
+    gemv_w4_body<BT, LPR, NCH, RPS, MODE, XM, LOOP>(kernel_params());
+}
+
+// O projection with the flash-decode combine in its staging: the number of
+// splits to read follows from the control block's position (block-uniform),
+// one straight-line body per count.  256 threads, 16 rows per block.
+template <int NCH>
+__global__ __launch_bounds__(256) void gemv_attn_o_kernel(GemvParams) {
+    const GemvParams& p = kernel_params();
+    const int live = p.ctl != nullptr ? flash_live_splits(min(p.ctl->seq_pos + 1, p.max_seq)) : kFlashSplits;
+    if (live <= 4) gemv_w4_body<256, 16, NCH, 1, kPlain, kXATTN4, false>(p);
+    else if (live <= 8) gemv_w4_body<256, 16, NCH, 1, kPlain, kXATTN8, false>(p);
+    else gemv_w4_body<256, 16, NCH, 1, kPlain, kXATTN16, false>(p);
 }
 
 // Generic kernel: one wave per output (row or SwiGLU pair), dword weight
@@ -963,14 +1006,13 @@ namespace {
 constexpr int kMaxAttnK = 2048;  // one 8-element unit per thread of a 256-thread block
 
 int launch_attn_o(const GemvParams& p, hipStream_t s) {
-    const Plan pl = plan_for(p.K, p.n_rows, kPlain, true);
-    if (pl.lpr != 16 || pl.bt != 256 || pl.rps != 1) return 0;
-    switch (pl.nch) {
-        case 2: return launch_fast<kPlain, kXATTN, 256, 16, 2, 1>(p, s);
-        case 3: return launch_fast<kPlain, kXATTN, 256, 16, 3, 1>(p, s);
-        case 6: return launch_fast<kPlain, kXATTN, 256, 16, 6, 1>(p, s);
-    }
-    return 0;
+    const int KC = p.K / 32;
+    const int grid = (p.n_rows + 15) / 16;
+    const size_t lds = static_cast<size_t>(p.K) + KC * 8 + 32;
+    if (KC <= 32) gemv_attn_o_kernel<2><<<grid, 256, lds, s>>>(p);
+    else if (KC <= 48) gemv_attn_o_kernel<3><<<grid, 256, lds, s>>>(p);
+    else gemv_attn_o_kernel<6><<<grid, 256, lds, s>>>(p);
+    return grid;
 }
 }  // namespace
 }  // namespace qe
@@ -978,8 +1020,10 @@ int launch_attn_o(const GemvParams& p, hipStream_t s) {
 extern "C" int qe_launch_attention_combine_gemv_o_w4a8(const float* splitk_partial_out,
                                                        const float* splitk_partial_lse, const uint32_t* o_qweight,
                                                        const uint16_t* o_scales, const uint16_t* residual,
-                                                       uint16_t* output_y, uint16_t* attn_out_opt, int out_features,
-                                                       int num_q_heads, int head_dim, hipStream_t stream) {
+                                                       uint16_t* output_y, uint16_t* attn_out_opt,
+                                                       const qe_device_control_block* d_control, int out_features,
+                                                       int num_q_heads, int head_dim, int max_seq_len,
+                                                       hipStream_t stream) {
     const char* what = "attention_combine_gemv_o_w4a8";
     QE_REQUIRE(splitk_partial_out && splitk_partial_lse && o_qweight && o_scales && output_y, "%s: NULL pointer",
                what);
@@ -988,6 +1032,7 @@ extern "C" int qe_launch_attention_combine_gemv_o_w4a8(const float* splitk_parti
     QE_REQUIRE(num_q_heads > 0 && K <= kMaxAttnK, "%s: %d q heads (at most %d)", what, num_q_heads,
                kMaxAttnK / 128);
     QE_REQUIRE(out_features > 0, "%s: out_features=%d", what, out_features);
+    QE_REQUIRE(max_seq_len > 0, "%s: max_seq_len=%d", what, max_seq_len);
     QE_REQUIRE(aligned(splitk_partial_out, 16) && aligned(splitk_partial_lse, 16) && aligned(o_qweight, 16) &&
                    aligned(o_scales, 2) && aligned(residual, 2) && aligned(output_y, 2) && aligned(attn_out_opt, 16),
                "%s: misaligned buffer (partials, weights and attn_out 16-byte aligned)", what);
@@ -999,6 +1044,8 @@ extern "C" int qe_launch_attention_combine_gemv_o_w4a8(const float* splitk_parti
     p.part_o = splitk_partial_out;
     p.part_lse = splitk_partial_lse;
     p.norm_out = attn_out_opt;
+    p.ctl = d_control;
+    p.max_seq = max_seq_len;
     p.n_rows = out_features;
     p.K = K;
     if (!launch_attn_o(p, stream)) return fail(QE_ERR_UNSUPPORTED, "%s: no kernel for K=%d", what, K);

@@ -50,7 +50,7 @@ SIGNATURES = {
     "qe_launch_attention_gqa_flash_decode": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P],
     "qe_launch_attention_gqa_flash_decode_combine": [_P, _P, _P, _P, _I, _P, _P, _P],
     "qe_launch_attention_gqa_flash_decode_partials": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I],
-    "qe_launch_attention_combine_gemv_o_w4a8": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "qe_launch_attention_combine_gemv_o_w4a8": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "qe_launch_attention_gqa_prefill": [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I],
 }
 
@@ -323,11 +323,11 @@ def launch_attention_gqa_flash_decode_partials(q, layer_k_cache, layer_v_cache, 
 
 
 def launch_attention_combine_gemv_o_w4a8(splitk_partial_out, splitk_partial_lse, o_qweight, o_scales, residual,
-                                         output_y, attn_out=None, out_features=1536, num_q_heads=12, head_dim=128,
-                                         stream=None):
+                                         output_y, attn_out=None, d_control=None, out_features=1536, num_q_heads=12,
+                                         head_dim=128, max_seq_len=4096, stream=None):
     _call("qe_launch_attention_combine_gemv_o_w4a8", _ptr(splitk_partial_out), _ptr(splitk_partial_lse),
-          _ptr(o_qweight), _ptr(o_scales), _ptr(residual), _ptr(output_y), _ptr(attn_out), out_features,
-          num_q_heads, head_dim, _stream(stream))
+          _ptr(o_qweight), _ptr(o_scales), _ptr(residual), _ptr(output_y), _ptr(attn_out), _ptr(d_control),
+          out_features, num_q_heads, head_dim, max_seq_len, _stream(stream))
 
 
 def launch_attention_gqa_prefill(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, stream=None,

@@ -92,7 +92,7 @@ def _attn_ref(q, kc, vc, seq_len, group):
     return out
 
 
-@pytest.mark.parametrize("seq_pos", [0, 5, 300, 4095])
+@pytest.mark.parametrize("seq_pos", [0, 5, 63, 64, 300, 1024, 1100, 4095])
 def test_flash_decode_attention(qe, orc, seq_pos):
     nq, nkv, D, max_seq = 12, 2, 128, 4096
     rng = np.random.default_rng(seq_pos)
@@ -120,7 +120,8 @@ def test_flash_decode_attention(qe, orc, seq_pos):
 
 
 @pytest.mark.parametrize("nq,nkv,seq_pos,res", [(12, 2, 0, True), (12, 2, 300, True), (12, 2, 4095, False),
-                                                 (16, 2, 77, True), (8, 1, 1000, False), (4, 4, 17, True)])
+                                                 (16, 2, 77, True), (8, 1, 1000, False), (4, 4, 17, True),
+                                                 (12, 2, 63, False), (12, 2, 64, True), (12, 2, 1500, True)])
 def test_attention_combine_gemv_o_bit_identical(qe, orc, nq, nkv, seq_pos, res):
     """partials -> (combine + Q8_1 + O GEMV + residual) in one launch equals
     flash_decode (stage 1 + 2) -> gemv_w4a8 bit for bit; partial buffers start
@@ -151,15 +152,15 @@ def test_attention_combine_gemv_o_bit_identical(qe, orc, nq, nkv, seq_pos, res):
     assert np.array_equal(host(part).reshape(nq, 16, D)[live].view(np.uint32),
                           host(part2).reshape(nq, 16, D)[live].view(np.uint32))
     y, attn = empty(H, torch.float16), empty(K, torch.float16)
-    qe.launch_attention_combine_gemv_o_w4a8(part2, lse2, dqw, dsc, residual, y, attn, out_features=H, num_q_heads=nq,
-                                            head_dim=D)
+    qe.launch_attention_combine_gemv_o_w4a8(part2, lse2, dqw, dsc, residual, y, attn, ctl, out_features=H,
+                                            num_q_heads=nq, head_dim=D, max_seq_len=max_seq)
     assert np.array_equal(host(attn).view(np.uint16), host(out).view(np.uint16))
     assert np.array_equal(host(y).view(np.uint16), host(ref_y).view(np.uint16))
     # without the attention copy, in place on the residual (the engine's call)
     if res:
         r2 = residual.clone()
-        qe.launch_attention_combine_gemv_o_w4a8(part2, lse2, dqw, dsc, r2, r2, None, out_features=H, num_q_heads=nq,
-                                                head_dim=D)
+        qe.launch_attention_combine_gemv_o_w4a8(part2, lse2, dqw, dsc, r2, r2, None, None, out_features=H,
+                                                num_q_heads=nq, head_dim=D)  # no control block: all 16 read
         assert np.array_equal(host(r2).view(np.uint16), host(ref_y).view(np.uint16))
 
 
