@@ -311,7 +311,12 @@ int qe_stream_read(const void* data, size_t bytes, uint32_t* sink, hipStream_t s
  *   "gemm_tile" 0..4 (default 0 = chosen per shape) - force the prefill GEMM
  *   block tile: 1 64x64, 2 64x128, 3 128x64, 4 128x128 (rows x columns);
  *   "gemm_slices" 0..64 (default 0 = chosen per shape) - force the number of
- *   K slices.  Returns QE_ERR_INVALID_ARGUMENT for an unknown key or value. */
+ *   K slices;
+ *   "gemv_block" 0, 256, 512, 1024 (default 0 = chosen per shape) - force the
+ *   decode GEMV block size;
+ *   "gemv_grid_cap" 0..65536 (default 0 = 8 blocks of 256 threads per CU) -
+ *   largest decode GEMV grid; larger row counts loop over row sets.
+ *   Returns QE_ERR_INVALID_ARGUMENT for an unknown key or value. */
 int qe_set_tuning(const char* key, int value);
 
 #ifdef __cplusplus

@@ -197,7 +197,8 @@ __device__ __forceinline__ void flash_round(FlashState<GH>& S, const u32x4 (&qra
                 l += p;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const uint32_t vw = vr[st][i];
+                    // rows past the context may hold anything: never multiplied in
+                    const uint32_t vw = sc[h][st] == -INFINITY ? 0u : static_cast<uint32_t>(vr[st][i]);
                     const f16x2 v2 = __builtin_bit_cast(f16x2, vw);
                     o[2 * i] += p * static_cast<float>(v2.x);
                     o[2 * i + 1] += p * static_cast<float>(v2.y);
@@ -214,9 +215,10 @@ __device__ __forceinline__ void flash_round(FlashState<GH>& S, const u32x4 (&qra
 // One block: GH q heads (qh0..qh0+GH-1) of kv head kvh over positions [t0, t1)
 // with NT threads (NT/16 lane groups).
 template <int GH, int NT>
-__device__ __forceinline__ void flash_decode_split(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-                                                   const uint16_t* __restrict__ vc, float* __restrict__ part_o,
-                                                   float* __restrict__ part_lse, int kvh, int qh0, int split, int t0,
+__device__ __forceinline__ void flash_decode_split(const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+                                                   float* __restrict__ part_o, float* __restrict__ part_lse,
+                                                   const u32x4 (&qraw)[GH], u32x4 (&ka)[64 / (NT / 16)],
+                                                   u32x4 (&va)[64 / (NT / 16)], int kvh, int qh0, int split, int t0,
                                                    int t1, int max_seq) {
     constexpr int NG = NT / 16, kSteps = 64 / NG;
     const int gid = threadIdx.x >> 4, j = threadIdx.x & 15;  // lane group of the block, lane in the group
@@ -230,12 +232,6 @@ __device__ __forceinline__ void flash_decode_split(const uint16_t* __restrict__ 
             vr[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vc + base + static_cast<size_t>(t) * kHeadDim));
         }
     };
-    u32x4 qraw[GH];
-#pragma unroll
-    for (int h = 0; h < GH; ++h) qraw[h] = *reinterpret_cast<const u32x4*>(q + (qh0 + h) * kHeadDim + 8 * j);
-    u32x4 ka[kSteps], va[kSteps];
-    load_round(t0, ka, va);
-    __builtin_amdgcn_sched_barrier(0);
     QE_TS(2, true);
     FlashState<GH> S;
 #pragma unroll
@@ -331,9 +327,29 @@ __global__ __launch_bounds__(NT) void flash_decode_stage1_kernel(const uint16_t*
                                                                  float* __restrict__ part_lse,
                                                                  const qe_device_control_block* ctl, int group,
                                                                  int max_seq) {
+    constexpr int NG = NT / 16, kSteps = 64 / NG;
     const int qh0 = blockIdx.x * GH, split = blockIdx.y;
     const int kvh = qh0 / group;
+    const int gid = threadIdx.x >> 4, j = threadIdx.x & 15;
+    QE_TS(7, false);
     QE_TS(0, false);
+    // q and the split's first 64 rows are requested before the position is
+    // known: with splits of 64 positions (contexts up to 16 * 64) the rows are
+    // those of split * 64 onwards; rows past the context are masked later
+    u32x4 qraw[GH];
+#pragma unroll
+    for (int h = 0; h < GH; ++h) qraw[h] = *reinterpret_cast<const u32x4*>(q + (qh0 + h) * kHeadDim + 8 * j);
+    u32x4 ka[kSteps], va[kSteps];
+    {
+        const size_t base = static_cast<size_t>(kvh) * max_seq * kHeadDim + 8 * j;
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+            const int t = min(split * kFlashMinSplit + st * NG + gid, max_seq - 1);
+            ka[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kc + base + static_cast<size_t>(t) * kHeadDim));
+            va[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vc + base + static_cast<size_t>(t) * kHeadDim));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
     const int seq_pos = ctl != nullptr ? ctl->seq_pos : 0;
     const int seq_len = min(seq_pos + 1, max_seq);
     const int per = flash_split_len(seq_len);
@@ -349,7 +365,16 @@ __global__ __launch_bounds__(NT) void flash_decode_stage1_kernel(const uint16_t*
         }
         return;
     }
-    flash_decode_split<GH, NT>(q, kc, vc, part_o, part_lse, kvh, qh0, split, t0, t1, max_seq);
+    if (per != kFlashMinSplit) {  // longer splits: the first round starts elsewhere
+        const size_t base = static_cast<size_t>(kvh) * max_seq * kHeadDim + 8 * j;
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {
+            const int t = min(t0 + st * NG + gid, t1 - 1);
+            ka[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kc + base + static_cast<size_t>(t) * kHeadDim));
+            va[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vc + base + static_cast<size_t>(t) * kHeadDim));
+        }
+    }
+    flash_decode_split<GH, NT>(kc, vc, part_o, part_lse, qraw, ka, va, kvh, qh0, split, t0, t1, max_seq);
 }
 
 // ---- flash decode, stage 2 + Q8_1 epilogue ---------------------------------------

@@ -49,6 +49,24 @@ constexpr int kXATTN16 = 5;
 
 constexpr float kRmsEps = 1e-6f;  // RMS_NORM_EPS, include/config.cuh:20
 
+// QE_GEMV_TIMING=1 builds a timing probe: per-block phase timestamps
+// (s_memrealtime, 100 MHz) into g_dbg_gemv, read back with qe_debug_gemv_ts.
+#if QE_GEMV_TIMING
+__device__ unsigned long long g_dbg_gemv[6][4096][8];
+#define QE_GTS(i, wait)                                                                      \
+    do {                                                                                     \
+        if (wait) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");               \
+        __builtin_amdgcn_sched_barrier(0);                                                   \
+        const unsigned long long t_ = __builtin_amdgcn_s_memrealtime();                      \
+        if (threadIdx.x == 0 && blockIdx.x < 4096) g_dbg_gemv[TS_KIND][blockIdx.x][i] = t_; \
+        __builtin_amdgcn_sched_barrier(0);                                                   \
+    } while (0)
+#else
+#define QE_GTS(i, wait) \
+    do {                \
+    } while (0)
+#endif
+
 struct GemvParams {
     const uint32_t* qw[3];
     const uint16_t* sc[3];
@@ -216,6 +234,52 @@ __device__ __forceinline__ void row_ptrs(const GemvParams& p, int row, int urow,
     }
     w = reinterpret_cast<const u32x4*>(qw + static_cast<size_t>(local) * (p.K >> 3));
     s = sc + static_cast<size_t>(local) * (p.K >> 7);
+}
+
+// QKV: the per-matrix kernel arguments, loaded together at entry and held in
+// scalar registers (the asm makes their values opaque, so the compiler does
+// not re-derive a selected pointer as a dependent load from the argument
+// block later).
+// Global (address space 1) pointer types: after the asm the compiler cannot
+// see where a pointer came from, and a generic one would be read with flat
+// loads (which also count against the scalar-load counter).
+typedef const uint32_t __attribute__((address_space(1)))* g_u32p;
+typedef const uint16_t __attribute__((address_space(1)))* g_u16p;
+typedef uint16_t __attribute__((address_space(1)))* g_u16p_mut;
+
+struct QkvArgs {
+    g_u32p qw[3];
+    g_u16p sc[3];
+    g_u16p bias[3];
+    g_u16p_mut out[3];
+    int rb1, rb2;
+};
+
+__device__ __forceinline__ QkvArgs load_qkv_args(const GemvParams& p) {
+    QkvArgs a{{(g_u32p)p.qw[0], (g_u32p)p.qw[1], (g_u32p)p.qw[2]},
+              {(g_u16p)p.sc[0], (g_u16p)p.sc[1], (g_u16p)p.sc[2]},
+              {(g_u16p)p.bias[0], (g_u16p)p.bias[1], (g_u16p)p.bias[2]},
+              {(g_u16p_mut)p.out[0], (g_u16p_mut)p.out[1], (g_u16p_mut)p.out[2]},
+              p.row_begin[1],
+              p.row_begin[2]};
+    asm volatile("" : "+s"(a.qw[0]), "+s"(a.qw[1]), "+s"(a.qw[2]), "+s"(a.sc[0]), "+s"(a.sc[1]), "+s"(a.sc[2]),
+                 "+s"(a.bias[0]), "+s"(a.bias[1]), "+s"(a.bias[2]), "+s"(a.out[0]), "+s"(a.out[1]), "+s"(a.out[2]),
+                 "+s"(a.rb1), "+s"(a.rb2));
+    return a;
+}
+
+template <typename T>
+__device__ __forceinline__ T pick3(const T (&v)[3], int m) {
+    return m == 0 ? v[0] : (m == 1 ? v[1] : v[2]);
+}
+
+__device__ __forceinline__ void row_ptrs_qkv(const QkvArgs& a, int K, int row, int urow, const u32x4*& w,
+                                             const uint16_t*& s, int& m, int& local) {
+    const int u = __builtin_amdgcn_readfirstlane(urow);
+    m = (u >= a.rb1) + (u >= a.rb2);
+    local = row - (m == 0 ? 0 : (m == 1 ? a.rb1 : a.rb2));
+    w = reinterpret_cast<const u32x4*>((const uint32_t*)(pick3(a.qw, m) + static_cast<size_t>(local) * (K >> 3)));
+    s = (const uint16_t*)(pick3(a.sc, m) + static_cast<size_t>(local) * (K >> 7));
 }
 
 // Q8_1 activation staged by the whole block: thread t copies chunk
@@ -421,6 +485,10 @@ __device__ __forceinline__ int rope_row(int set) {
 
 template <int BT, int LPR, int NCH, int RPS, int MODE, int XM, bool LOOP>
 __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
+#if QE_GEMV_TIMING
+    constexpr int TS_KIND = MODE == kQKV ? 0 : (is_attn(XM) ? 1 : (MODE == kSwiglu ? 2 : (MODE == kSample ? 4 : 3)));
+#endif
+    QE_GTS(7, false);
     // SwiGLU: a segment owns a (gate, up) row pair (RPS 2), or, with 16-lane
     // segments and RPS 1, segments 2s and 2s+1 own the gate and up row and
     // meet through a 32-lane swizzle
@@ -433,6 +501,7 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
     const int l = threadIdx.x % LPR;
     const int n_sets = (p.n_rows + RPS - 1) / RPS;
     const int set_stride = SEGS * gridDim.x;
+    QE_GTS(0, false);
 
     // ---- activation loads first (a few KB, needed first), then the first
     //      row set's weights; the activation math overlaps the weight stream.
@@ -453,7 +522,32 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
     if constexpr (XM == kXQ8) stage_issue_q8<BT, MQ>(p, qa, qb, qs4, qxd);
     else if constexpr (is_attn(XM)) stage_issue_attn<LS>(p, apo, apl);
     else stage_issue_f16<XM, BT, MAXP>(p, raw, graw);
+    constexpr bool ROPE_EPI = MODE == kQKV && LPR == 16 && RPS == 1 && BT == 256 && !LOOP;
+    QkvArgs qka{};
+    if constexpr (MODE == kQKV) qka = load_qkv_args(p);
+    uint16_t rope_bias = 0;  // fp16 bits of this lane's row bias (QKV with RoPE)
+    int rope_pos = 0;        // the position (clamped later)
+    if constexpr (ROPE_EPI) {
+        // requested here, ahead of the weights (first used after the GEMV)
+        if (p.rope) {
+            const int row = rope_row(min(blockIdx.x * SEGS + seg, n_sets - 1));
+            const int u = __builtin_amdgcn_readfirstlane(row & ~127);
+            const int m = (u >= qka.rb1) + (u >= qka.rb2);
+            const int local = row - (m == 0 ? 0 : (m == 1 ? qka.rb1 : qka.rb2));
+            const g_u16p b = pick3(qka.bias, m);
+            rope_bias = b != nullptr ? b[local] : 0;
+            typedef const int __attribute__((address_space(1)))* g_i32p;
+            rope_pos = p.ctl != nullptr ? *(g_i32p)&p.ctl->seq_pos : 0;
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+#if QE_GEMV_ISSUE_BARRIER
+    // every wave's activation loads are issued before any wave's weight loads:
+    // the staging barrier below waits for the activation of all waves, which
+    // would otherwise queue behind other waves' weight loads
+    if constexpr (BT > 64) __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#endif
 
     int set = blockIdx.x * SEGS + seg;
     u32x4 w[RPS][NCH];
@@ -470,7 +564,8 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
             const u32x4* wp;
             const uint16_t* sp;
             int m, local;
-            row_ptrs<MODE>(p, row, urow, wp, sp, m, local);
+            if constexpr (MODE == kQKV) row_ptrs_qkv(qka, p.K, row, urow, wp, sp, m, local);
+            else row_ptrs<MODE>(p, row, urow, wp, sp, m, local);
 #pragma unroll
             for (int i = 0; i < NCH; ++i) {
                 const int c = min(l + i * LPR, KC - 1);
@@ -481,6 +576,17 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
     };
     load_set(min(set, n_sets - 1), w, hs);
     __builtin_amdgcn_sched_barrier(0);
+    QE_GTS(1, false);
+    // QKV with RoPE: position and angle of this lane's row, while the loads
+    // are in flight (the bias was requested with the activation, ahead of the
+    // weights, so using it does not wait for them)
+    float rope_sn = 0.0f, rope_cs = 1.0f;
+    if constexpr (ROPE_EPI) {
+        if (p.rope) {
+            rope_pos = rope_pos < p.max_seq ? rope_pos : p.max_seq - 1;
+            rope_sincos(rope_pos, rope_row(min(set, n_sets - 1)) & 63, 128, p.rope_theta, rope_sn, rope_cs);
+        }
+    }
 
     // ---- activation slice in VGPRs, through LDS ----------------------------------
     {
@@ -533,31 +639,29 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
             acc[r] = qwen::seg_sum<LPR>(a);
         }
         if constexpr (PAIR) acc[0] = silu_mul(acc[0], qwen::swz_xor16_f32(acc[0]));  // gate (even set) x up
-        if constexpr (MODE == kQKV && LPR == 16 && RPS == 1 && BT == 256 && !LOOP) {
+        if constexpr (ROPE_EPI) {
             if (p.rope) {  // block-uniform: one pass over 16-row groups of one head
                 __shared__ uint16_t s_rv[16];
                 const int row = rope_row(st);
-                const int m = (row >= p.row_begin[1]) + (row >= p.row_begin[2]);
-                const int local = row - (m == 0 ? 0 : (m == 1 ? p.row_begin[1] : p.row_begin[2]));
-                const uint16_t* b = m == 0 ? p.bias[0] : (m == 1 ? p.bias[1] : p.bias[2]);
-                // GEMV output rounded to fp16, then the bias added in fp16 (as the separate kernels do)
+                const int u = __builtin_amdgcn_readfirstlane(row & ~127);
+                const int m = (u >= qka.rb1) + (u >= qka.rb2);
+                const int local = row - (m == 0 ? 0 : (m == 1 ? qka.rb1 : qka.rb2));
+                // GEMV output rounded to fp16, then the bias (loaded at entry) added in fp16,
+                // as the separate kernels do
+                const bool has_bias = pick3(qka.bias, m) != nullptr;
                 _Float16 v = static_cast<_Float16>(acc[0]);
-                if (b != nullptr) v = v + __builtin_bit_cast(_Float16, b[local]);
+                if (has_bias) v = v + __builtin_bit_cast(_Float16, rope_bias);
                 if (l == 0) s_rv[seg] = __builtin_bit_cast(uint16_t, v);
                 __syncthreads();
                 if (l == 0) {
-                    const int pos0 = p.ctl != nullptr ? p.ctl->seq_pos : 0;
-                    const int pos = pos0 < p.max_seq ? pos0 : p.max_seq - 1;
+                    const int pos = rope_pos;
                     const int e = local & 127, head = local >> 7;
                     uint16_t outv = __builtin_bit_cast(uint16_t, v);
                     if (m < 2) {  // q and k rows rotate with their partner (segment s ^ 8)
-                        float sn, cs;
-                        rope_sincos(pos, e & 63, 128, p.rope_theta, sn, cs);
                         const float y = h2f(s_rv[seg ^ 8]);
-                        outv = f2h(rope_rotate(static_cast<float>(v), y, e < 64, sn, cs));
+                        outv = f2h(rope_rotate(static_cast<float>(v), y, e < 64, rope_sn, rope_cs));
                     }
-                    uint16_t* o = m == 0 ? p.out[0] : (m == 1 ? p.out[1] : p.out[2]);
-                    o[local] = outv;
+                    pick3(qka.out, m)[local] = outv;
                     if (m > 0) {
                         uint16_t* cache = m == 1 ? p.kcache : p.vcache;
                         cache[(static_cast<size_t>(head) * p.max_seq + pos) * 128 + e] = outv;
@@ -584,19 +688,24 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
                         const u32x4* wp;
                         const uint16_t* sp;
                         int m, local;
-                        row_ptrs<MODE>(p, row, (st - seg) * RPS, wp, sp, m, local);
+                        if constexpr (MODE == kQKV) row_ptrs_qkv(qka, p.K, row, (st - seg) * RPS, wp, sp, m, local);
+                        else row_ptrs<MODE>(p, row, (st - seg) * RPS, wp, sp, m, local);
                         float v = acc[r];
                         if (MODE == kPlain && p.residual != nullptr) v += h2f(p.residual[local]);
                         uint16_t* o = p.out[0];
-                        if constexpr (MODE == kQKV) o = m == 0 ? p.out[0] : (m == 1 ? p.out[1] : p.out[2]);
+                        if constexpr (MODE == kQKV) o = (uint16_t*)pick3(qka.out, m);
                         o[local] = f2h(v);
                     }
                 }
             }
         }
     };
+    QE_GTS(2, false);
     if constexpr (!LOOP) {
+        QE_GTS(3, true);
         finish_set(set);  // the grid covers every set once
+        QE_GTS(4, false);
+        QE_GTS(5, true);
     } else {
         for (; set < n_sets; set += set_stride) {
             u32x4 wn[RPS][NCH];
@@ -742,6 +851,7 @@ int launch_fast(const GemvParams& p, hipStream_t s) {
     const int sets = (p.n_rows + RPS - 1) / RPS;
     int grid = (sets + SEGS - 1) / SEGS;
     int cap = cu_count() * 8 * 256 / BT;
+    if (const int f = gemv_forced_cap()) cap = f;
     if (MODE == kSample && cap > QE_LM_HEAD_SAMPLE_PARTS) cap = QE_LM_HEAD_SAMPLE_PARTS;
     const size_t lds = static_cast<size_t>(p.K) + (p.K >> 5) * 8 + 32;  // + dummy slot
     if (grid > cap) {
@@ -1051,6 +1161,12 @@ extern "C" int qe_launch_attention_combine_gemv_o_w4a8(const float* splitk_parti
     if (!launch_attn_o(p, stream)) return fail(QE_ERR_UNSUPPORTED, "%s: no kernel for K=%d", what, K);
     return check_launch(what);
 }
+
+#if QE_GEMV_TIMING
+extern "C" int qe_debug_gemv_ts(void* host) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(qe::g_dbg_gemv), sizeof(qe::g_dbg_gemv)) == hipSuccess ? 0 : 1;
+}
+#endif
 
 // ---- fused LM head + sampling ------------------------------------------------------
 namespace qe {

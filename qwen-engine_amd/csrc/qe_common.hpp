@@ -27,6 +27,7 @@ int gemm_split_k_enabled();
 int gemm_forced_tile();    // 0 auto, 1 64x64, 2 64x128 (1x4 waves), 3 128x64, 4 128x128 (1x4 waves)
 int gemm_forced_slices();  // 0 auto, else K slices
 int gemv_forced_bt();      // 0 auto, else GEMV block size (256, 512, 1024)
+int gemv_forced_cap();     // 0 auto, else the largest GEMV grid (larger grids loop over row sets)
 
 inline int fail(int code, const char* fmt, ...) {
     char buf[512];

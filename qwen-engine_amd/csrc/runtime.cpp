@@ -18,12 +18,14 @@ int g_gemm_split_k = 1;
 int g_gemm_tile = 0;
 int g_gemm_slices = 0;
 int g_gemv_bt = 0;
+int g_gemv_cap = 0;
 }  // namespace
 
 int gemm_split_k_enabled() { return g_gemm_split_k; }
 int gemm_forced_tile() { return g_gemm_tile; }
 int gemm_forced_slices() { return g_gemm_slices; }
 int gemv_forced_bt() { return g_gemv_bt; }
+int gemv_forced_cap() { return g_gemv_cap; }
 
 void set_error(const char* fmt, ...) {
     va_list ap;
@@ -66,6 +68,12 @@ extern "C" int qe_set_tuning(const char* key, int value) {
         if (value != 0 && value != 256 && value != 512 && value != 1024)
             return qe::fail(QE_ERR_INVALID_ARGUMENT, "set_tuning: gemv_block %d not in {0, 256, 512, 1024}", value);
         qe::g_gemv_bt = value;
+        return QE_OK;
+    }
+    if (std::strcmp(key, "gemv_grid_cap") == 0) {
+        if (value < 0 || value > 65536)
+            return qe::fail(QE_ERR_INVALID_ARGUMENT, "set_tuning: gemv_grid_cap %d not in 0..65536", value);
+        qe::g_gemv_cap = value;
         return QE_OK;
     }
     if (std::strcmp(key, "gemm_slices") == 0) {
