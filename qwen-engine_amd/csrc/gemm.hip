@@ -192,7 +192,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
         for (int j = 0; j < NI; ++j) {
 #pragma unroll
             for (int i = 0; i < (QUAD ? 4 : 1); ++i)
-                rb[e][j][i] = __builtin_nontemporal_load(b_src[j] + (QUAD ? 8 * g + i : 2 * g));
+                rb[e][j][i] = b_src[j][QUAD ? 8 * g + i : 2 * g];  // cached: every M tile of the column reads it
             rs[e][j] = b_sc[j][QUAD ? 2 * g : (g >> 1)];
         }
     };
@@ -337,10 +337,10 @@ struct TileCost {
     float fixed;
 };
 constexpr TileCost kTiles[4] = {
-    {64, 64, 2, 0.464f, 0.912f, 5.50f, 0.030f, 1.34f},
-    {64, 128, 1, 0.521f, 1.112f, 6.06f, 0.024f, 3.74f},
-    {128, 64, 2, 0.588f, 1.224f, 6.23f, 0.018f, 4.07f},
-    {128, 128, 1, 0.688f, 1.632f, 33.7f, 0.020f, 7.57f},
+    {64, 64, 2, 0.277f, 0.543f, 3.85f, 0.014f, 4.80f},
+    {64, 128, 1, 0.321f, 0.683f, 5.37f, 0.012f, 5.24f},
+    {128, 64, 2, 0.410f, 0.845f, 5.41f, 0.018f, 5.24f},
+    {128, 128, 1, 0.535f, 1.152f, 29.8f, 0.0f, 6.50f},
 };
 
 float predict_us(const TileCost& t, int M, int N, int K, int slices, int cus) {
@@ -462,8 +462,8 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a8_mfma_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             S.s8[j] = *reinterpret_cast<const i32x4*>(p.A8_sum8 + srow_g * (K >> 3) + 16 * g + 4 * j);
-        S.b[0] = __builtin_nontemporal_load(b_src + 4 * g);
-        S.b[1] = __builtin_nontemporal_load(b_src + 4 * g + 1);
+        S.b[0] = b_src[4 * g];  // cached: every M tile of the column reads it
+        S.b[1] = b_src[4 * g + 1];
         S.bs = b_sc[g];
     };
     auto store = [&](int buf, const Stage& S) __attribute__((always_inline)) {
