@@ -49,6 +49,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-step", action="store_true", help="headline step only (for profiling)")
     ap.add_argument("--only-roofline", action="store_true", help="dominant kernel's timing only (for profiling)")
+    ap.add_argument("--only-prefill-gemm", type=int, default=0, metavar="M",
+                    help="configs[3] gate/up GEMM at M tokens only, 20 launches (for profiling)")
+    ap.add_argument("--only-decode", action="store_true",
+                    help="configs[4] engine decode only: prompt 128, 64 graph tokens (for profiling)")
     ap.add_argument("--calib-read", action="store_true",
                     help="with --only-step: also stream-read 64 MiB 5 times (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -102,6 +106,25 @@ def main():
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / replays  # ms per graph
+
+    if args.only_prefill_gemm:
+        M = args.only_prefill_gemm
+        qw, sc = rand_w4(2 * I, H, 1)
+        A = torch.randn((M, H), device=dev, generator=gen).half()
+        outp = torch.empty((M, I), dtype=torch.float16, device=dev)
+        for _ in range(20):
+            qe_amd.launch_gemm_prefill_dual_gate_up_swiglu_w4a16(qw[0], sc[0], A, outp, M, hidden_size=H,
+                                                                 intermediate_size=I)
+        torch.cuda.synchronize()
+        print(json.dumps({"only_prefill_gemm": {"M": M, "N": 2 * I, "K": H, "launches": 20}}))
+        return
+    if args.only_decode:
+        eng = qe_amd.Engine(qe_amd.default_config(), seed=2024)
+        eng.prefill(np.random.default_rng(128).integers(0, V, 128).tolist())
+        toks, step_ms = eng.decode(64, use_graph=True, timed=True)
+        eng.close()
+        print(json.dumps({"only_decode": {"tokens": 64, "itl_ms_p50": sorted(step_ms)[len(step_ms) // 2]}}))
+        return
 
     # ---------------- activations / scratch ----------------------------------
     x = torch.randn(H, device=dev, generator=gen).half()
