@@ -26,6 +26,8 @@
 //     persistent blocks (grid capped per CU).
 // Shapes outside the fast kernel (weights not 16-byte aligned, K > 16384)
 // use a generic wave-per-row kernel that stages Q8_1 in LDS.
+#include <algorithm>
+
 #include "attn_common.hpp"
 #include "rope_common.hpp"
 #include "sample_common.hpp"
@@ -851,6 +853,10 @@ int launch_fast(const GemvParams& p, hipStream_t s) {
     const int sets = (p.n_rows + RPS - 1) / RPS;
     int grid = (sets + SEGS - 1) / SEGS;
     int cap = cu_count() * 8 * 256 / BT;
+    // fp16 input: every block quantizes (and RMS-normalizes) the whole
+    // activation, so fewer, looping blocks win once the grid exceeds three per
+    // CU (measured: RMSNorm+gate/up 1536 -> 2x8960 5.6 -> 4.9 us)
+    if constexpr (XM == kXF16 || XM == kXRMS) cap = std::min(cap, 3 * cu_count());
     if (const int f = gemv_forced_cap()) cap = f;
     if (MODE == kSample && cap > QE_LM_HEAD_SAMPLE_PARTS) cap = QE_LM_HEAD_SAMPLE_PARTS;
     const size_t lds = static_cast<size_t>(p.K) + (p.K >> 5) * 8 + 32;  // + dummy slot
