@@ -19,9 +19,6 @@ constexpr int kSplits = kFlashSplits;
 constexpr int kHeadDim = 128;
 constexpr int kVocab = 151936;  // VOCAB_SIZE: out-of-range token ids map to 0
 
-__device__ __forceinline__ float2 h2f2(uint32_t w) {
-    return make_float2(h2f(static_cast<uint16_t>(w & 0xFFFFu)), h2f(static_cast<uint16_t>(w >> 16)));
-}
 
 // ---- embedding ---------------------------------------------------------------
 __global__ __launch_bounds__(256) void embed_lookup_w4a16_kernel(const uint32_t* __restrict__ qw,
@@ -418,80 +415,148 @@ __global__ __launch_bounds__(128) void flash_decode_stage2_kernel(const float* _
     if ((tid & 7) == 0 && q_sum8 != nullptr) q_sum8[qh * (kHeadDim / 8) + (tid >> 3)] = s8;
 }
 
-// ---- causal prefill attention ----------------------------------------------------
-// grid (num_q_heads, ceil(T/16)), 256 threads: wave w owns query rows
-// 4w..4w+3 of the 16-row tile; lane l holds dims 2l, 2l+1.  K/V tiles of 32
-// positions are staged in LDS.  Query m sits at position base + m and sees
-// keys [0, base + m].
-__global__ __launch_bounds__(256) void prefill_attention_kernel(const uint16_t* __restrict__ q,
-                                                                const uint16_t* __restrict__ kc,
-                                                                const uint16_t* __restrict__ vc,
-                                                                uint16_t* __restrict__ out,
-                                                                const qe_device_control_block* ctl, int T, int nq,
-                                                                int nkv, int max_seq, int out_stride) {
-    constexpr int BR = 16, BC = 32;
-    const int qh = blockIdx.x;
-    const int m0 = blockIdx.y * BR;
-    const int group = nq / nkv;
-    const int kvh = qh / group;
-    const int base = ctl != nullptr ? ctl->seq_pos : 0;
+// ---- causal prefill attention (matrix cores) ---------------------------------------
+// grid (num_kv_heads, ceil(T/32)), GROUP waves: wave w is q head kvh*GROUP + w,
+// the block's 32 queries are m0..m0+31 (position base + m; keys [0, base + m]).
+// v_mfma_f32_32x32x16_f16 with queries as the columns:
+//   S^T (32 keys x 32 queries) = K (keys x 128 dims) . Q^T — lane l holds key
+//   row l%32 / query column l%32, dims 8*(l/32) + 16*kk: one 16-byte load each
+//   from the K cache and from q, no LDS;
+//   the result has lane l = query l%32 holding 16 keys (8*(v/4) + 4*(l/32) +
+//   v%4), so a query's max and sum are 16 in-lane values plus one lane^32 swap;
+//   O^T (128 dims x 32 queries) += V^T . P^T — P^T is the lane's own 16
+//   probabilities (fp16, k order = the keys it holds; the k order inside an
+//   MFMA is free when both operands agree) and V^T comes from an LDS tile the
+//   block stores transposed (two 8-byte reads per MFMA).
+// Online softmax in the exp2 domain, fp32 accumulation; the output is O / L.
+constexpr int kPqTile = 32;      // queries per block
+constexpr int kPkTile = 32;      // keys per step
+constexpr int kVtStride = 40;    // halves per LDS row of V^T (32 keys + 8 pad)
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int GROUP>
+__global__ __launch_bounds__(64 * GROUP) void prefill_attention_mfma_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    uint16_t* __restrict__ out, const qe_device_control_block* ctl, int T, int nq, int max_seq, int out_stride) {
+    constexpr int NT = 64 * GROUP;
+    __shared__ __align__(16) uint16_t sVt[2][kHeadDim * kVtStride];
+    const int kvh = blockIdx.x, m0 = blockIdx.y * kPqTile;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int q_dim = nq * kHeadDim;
-    int qpos[4];
-    float2 qv[4], o[4];
-    float mi[4], di[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wave * 4 + r;
-        qpos[r] = m < T ? min(base + m, max_seq - 1) : -1;
-        qv[r] = m < T ? h2f2(reinterpret_cast<const uint32_t*>(q + static_cast<size_t>(m) * q_dim + qh * kHeadDim)[lane])
-                      : make_float2(0, 0);
-        o[r] = make_float2(0, 0);
-        mi[r] = -INFINITY;
-        di[r] = 0.0f;
-    }
-    const int last = min(m0 + BR - 1, T - 1);
-    const int kv_len = min(base + last, max_seq - 1) + 1;
-    __shared__ __align__(16) uint32_t sK[BC][kHeadDim / 2], sV[BC][kHeadDim / 2];
-    const float scale = 1.0f / sqrtf(static_cast<float>(kHeadDim));
+    const int qh = kvh * GROUP + wave;
+    const int fr = lane & 31, h = lane >> 5;
+    const int base = ctl != nullptr ? ctl->seq_pos : 0;
+    const int m = m0 + fr;                       // this lane's query
+    const int qpos = base + m;                    // its position
+    const int last = min(m0 + kPqTile - 1, T - 1);
+    const int kv_len = min(base + last + 1, max_seq);
     const size_t hb = static_cast<size_t>(kvh) * max_seq * kHeadDim;
-    for (int tb = 0; tb < kv_len; tb += BC) {
-        const int len = min(BC, kv_len - tb);
-        for (int i = threadIdx.x; i < len * 16; i += 256) {
-            const int r = i >> 4, c = i & 15;
-            const size_t src = hb + static_cast<size_t>(tb + r) * kHeadDim + c * 8;
-            *reinterpret_cast<uint4*>(&sK[r][c * 4]) = *reinterpret_cast<const uint4*>(kc + src);
-            *reinterpret_cast<uint4*>(&sV[r][c * 4]) = *reinterpret_cast<const uint4*>(vc + src);
-        }
-        __syncthreads();
-        for (int j = 0; j < len; ++j) {
-            const int kp = tb + j;
-            const float2 kv = h2f2(sK[j][lane]);
-            const float2 vv = h2f2(sV[j][lane]);
+    constexpr float kScale = 1.4426950408889634f * 0.08838834764831845f;  // log2(e) / sqrt(128)
+
+    // Q^T operand: 8 k-steps of 16 dims, 8 halves per lane
+    u32x4 qf[8];
+    {
+        const uint16_t* qr = q + static_cast<size_t>(min(m, T - 1)) * (static_cast<size_t>(nq) * kHeadDim) +
+                             qh * kHeadDim + 8 * h;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (qpos[r] >= kp) {  // wave-uniform
-                    const float s = qwen::seg_sum<64>(qv[r].x * kv.x + qv[r].y * kv.y) * scale;
-                    const float mc = fmaxf(mi[r], s);
-                    const float alpha = expf(mi[r] - mc);
-                    const float beta = expf(s - mc);
-                    di[r] = di[r] * alpha + beta;
-                    o[r].x = o[r].x * alpha + beta * vv.x;
-                    o[r].y = o[r].y * alpha + beta * vv.y;
-                    mi[r] = mc;
-                }
+        for (int kk = 0; kk < 8; ++kk) qf[kk] = *reinterpret_cast<const u32x4*>(qr + 16 * kk);
+    }
+    f32x16 acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x16{};
+    float mrow = -INFINITY, lrow = 0.0f;
+
+    // V tile (32 keys x 128 dims) -> LDS as V^T: chunk c = (key c/16, dims 8*(c%16)..+7)
+    auto stage_v = [&](int t0, int buf) __attribute__((always_inline)) {
+        for (int c = threadIdx.x; c < kPkTile * 16; c += NT) {
+            const int key = c >> 4, d0 = 8 * (c & 15);
+            const int pos = min(t0 + key, max_seq - 1);
+            const u32x4 v = *reinterpret_cast<const u32x4*>(vc + hb + static_cast<size_t>(pos) * kHeadDim + d0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t w = v[e];
+                sVt[buf][(d0 + 2 * e) * kVtStride + key] = static_cast<uint16_t>(w & 0xFFFFu);
+                sVt[buf][(d0 + 2 * e + 1) * kVtStride + key] = static_cast<uint16_t>(w >> 16);
             }
         }
-        __syncthreads();
-    }
+    };
+    stage_v(0, 0);
+    __syncthreads();
+    int buf = 0;
+    for (int t0 = 0; t0 < kv_len; t0 += kPkTile) {
+        // S^T = K . Q^T
+        f32x16 sacc = f32x16{};
+        {
+            const int kpos = min(t0 + fr, max_seq - 1);
+            const uint16_t* kr = kc + hb + static_cast<size_t>(kpos) * kHeadDim + 8 * h;
+            u32x4 kf[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wave * 4 + r;
-        if (m < T) {
-            const float inv = di[r] > 0.0f ? 1.0f / di[r] : 0.0f;
-            const uint32_t w = static_cast<uint32_t>(f2h(o[r].x * inv)) | (static_cast<uint32_t>(f2h(o[r].y * inv)) << 16);
-            reinterpret_cast<uint32_t*>(out + static_cast<size_t>(m) * out_stride + qh * kHeadDim)[lane] = w;
+            for (int kk = 0; kk < 8; ++kk) kf[kk] = *reinterpret_cast<const u32x4*>(kr + 16 * kk);
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk)
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf[kk]),
+                                                              __builtin_bit_cast(f16x8, qf[kk]), sacc, 0, 0, 0);
         }
+        if (t0 + kPkTile < kv_len) stage_v(t0 + kPkTile, buf ^ 1);  // next tile, other buffer
+        // online softmax over this lane's 16 keys (+ the partner lane's 16)
+        float sv[16];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int key = t0 + 8 * (v >> 2) + 4 * h + (v & 3);
+            const bool ok = key < kv_len && key <= qpos && m < T;
+            sv[v] = ok ? sacc[v] * kScale : -INFINITY;
+            mx = fmaxf(mx, sv[v]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(mrow, mx);
+        const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mrow - mn);
+        mrow = mn;
+        float ps = 0.0f;
+        uint32_t pw[8];
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) {
+            const float p0 = sv[v] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[v] - mn);
+            const float p1 = sv[v + 1] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[v + 1] - mn);
+            ps += p0 + p1;
+            pw[v >> 1] = static_cast<uint32_t>(f2h(p0)) | (static_cast<uint32_t>(f2h(p1)) << 16);
+        }
+        lrow = lrow * alpha + ps;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[dt][v] *= alpha;
+        // O^T += V^T . P^T, two 16-key halves of the tile
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const u32x4 pf = {pw[4 * ks], pw[4 * ks + 1], pw[4 * ks + 2], pw[4 * ks + 3]};
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const uint16_t* row = &sVt[buf][(32 * dt + fr) * kVtStride + 16 * ks + 4 * h];
+                const uint2 lo = *reinterpret_cast<const uint2*>(row);      // keys 16ks + 4h .. +3
+                const uint2 hi = *reinterpret_cast<const uint2*>(row + 8);  // keys 16ks + 8 + 4h .. +3
+                const u32x4 vf = {lo.x, lo.y, hi.x, hi.y};
+                acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf),
+                                                                 __builtin_bit_cast(f16x8, pf), acc[dt], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // this tile's V^T is consumed; the next one is stored
+        buf ^= 1;
+    }
+    lrow += __shfl_xor(lrow, 32);
+    if (m < T) {
+        const float inv = lrow > 0.0f ? 1.0f / lrow : 0.0f;
+        uint16_t* o = out + static_cast<size_t>(m) * out_stride + qh * kHeadDim;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {  // dims 32dt + 8g + 4h .. +3
+                const uint32_t w0 = static_cast<uint32_t>(f2h(acc[dt][4 * g] * inv)) |
+                                    (static_cast<uint32_t>(f2h(acc[dt][4 * g + 1] * inv)) << 16);
+                const uint32_t w1 = static_cast<uint32_t>(f2h(acc[dt][4 * g + 2] * inv)) |
+                                    (static_cast<uint32_t>(f2h(acc[dt][4 * g + 3] * inv)) << 16);
+                *reinterpret_cast<uint2*>(o + 32 * dt + 8 * g + 4 * h) = make_uint2(w0, w1);
+            }
     }
 }
 
@@ -616,8 +681,17 @@ extern "C" int qe_launch_attention_gqa_prefill(const uint16_t* q, const uint16_t
     QE_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, "attention_gqa_prefill: bad head counts");
     QE_REQUIRE(hidden_size >= num_q_heads * head_dim, "attention_gqa_prefill: hidden_size=%d", hidden_size);
     if (num_tokens <= 0) return QE_OK;
-    prefill_attention_kernel<<<dim3(num_q_heads, (num_tokens + 15) / 16), 256, 0, stream>>>(
-        q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, num_q_heads, num_kv_heads, max_seq_len,
-        hidden_size);
+    QE_REQUIRE(aligned(q, 16) && aligned(attn_out, 8) && hidden_size % 4 == 0,
+               "attention_gqa_prefill: q must be 16-byte and attn_out 8-byte aligned");
+    const int group = num_q_heads / num_kv_heads;
+    const dim3 grid(num_kv_heads, (num_tokens + kPqTile - 1) / kPqTile);
+    switch (group) {
+        case 1: prefill_attention_mfma_kernel<1><<<grid, 64, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, num_q_heads, max_seq_len, hidden_size); break;
+        case 2: prefill_attention_mfma_kernel<2><<<grid, 128, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, num_q_heads, max_seq_len, hidden_size); break;
+        case 4: prefill_attention_mfma_kernel<4><<<grid, 256, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, num_q_heads, max_seq_len, hidden_size); break;
+        case 6: prefill_attention_mfma_kernel<6><<<grid, 384, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, num_q_heads, max_seq_len, hidden_size); break;
+        case 8: prefill_attention_mfma_kernel<8><<<grid, 512, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, num_q_heads, max_seq_len, hidden_size); break;
+        default: return fail(QE_ERR_UNSUPPORTED, "attention_gqa_prefill: %d q heads per kv head (built: 1, 2, 4, 6, 8)", group);
+    }
     return check_launch("attention_gqa_prefill");
 }

@@ -199,7 +199,7 @@ def test_qkv_bias_rope_kv_append(qe):
     assert np.all(gkc[:, base + T:] == 0) and np.all(gkc[:, :base] == 0)
 
 
-@pytest.mark.parametrize("T,base", [(1, 0), (37, 0), (128, 0), (20, 100)])
+@pytest.mark.parametrize("T,base", [(1, 0), (37, 0), (128, 0), (20, 100), (33, 31), (200, 300)])
 def test_prefill_attention(qe, T, base):
     nq, nkv, D, max_seq = 12, 2, 128, 512
     rng = np.random.default_rng(T + base)
