@@ -112,7 +112,7 @@ def test_gemv_swiglu_w4a8(qe, orc, I, K):
 
 
 @pytest.mark.parametrize("N,K", [(8960, 1536), (1536, 8960), (64, 128), (333, 2560), (50, 20480), (1001, 4096),
-                                 (7, 16384)])
+                                 (7, 16384), (20000, 1536), (13001, 8960)])
 def test_gemv_w4a16(qe, orc, N, K):
     """W4A16 GEMV 1536->8960 with in-launch Q8_1 quantization."""
     print(f"gemv_w4a16 N={N} K={K}", flush=True)
