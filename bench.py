@@ -57,8 +57,8 @@ def main():
                     help="with --only-step: also stream-read 64 MiB 5 times (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build runs on one GPU only (the W4A16 path has no multi-GPU "
-              "component; see DESIGN.md for how it would shard). Use --gpus 1.", file=sys.stderr)
+        print("bench.py: this build runs on one GPU only (the W4A16 path has no multi-GPU component; "
+              "it would shard by weight rows, one all-reduce after O and down). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
