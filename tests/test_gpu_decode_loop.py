@@ -199,9 +199,11 @@ def test_qkv_bias_rope_kv_append(qe):
     assert np.all(gkc[:, base + T:] == 0) and np.all(gkc[:, :base] == 0)
 
 
-@pytest.mark.parametrize("T,base", [(1, 0), (37, 0), (128, 0), (20, 100), (33, 31), (200, 300)])
-def test_prefill_attention(qe, T, base):
-    nq, nkv, D, max_seq = 12, 2, 128, 512
+@pytest.mark.parametrize("T,base,nq,nkv", [(1, 0, 12, 2), (37, 0, 12, 2), (128, 0, 12, 2), (20, 100, 12, 2),
+                                           (33, 31, 12, 2), (200, 300, 12, 2), (70, 5, 8, 1), (45, 0, 4, 4),
+                                           (64, 17, 4, 2)])
+def test_prefill_attention(qe, T, base, nq, nkv):
+    D, max_seq = 128, 512
     rng = np.random.default_rng(T + base)
     q = rng.standard_normal((T, nq * D)).astype(np.float16)
     kc = rng.standard_normal((nkv, max_seq, D)).astype(np.float16)
