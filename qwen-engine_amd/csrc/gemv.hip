@@ -477,12 +477,14 @@ __device__ __forceinline__ void stage_finish_attn(const GemvParams& p, const flo
     s_rec[(ok && (u & 3) == 0) ? (u >> 2) : KC] = make_int2(csum, __builtin_bit_cast(int, d));
 }
 
-// QKV with RoPE: set s of block group g = s / 16 covers head g / 8; its 16
-// segments take rows j*8 + t and 64 + j*8 + t (j = g % 8, t < 8) of that head
+// QKV with RoPE: set s of block group g = s / 16 covers head g / 8; its
+// segments 2t and 2t + 1 (t < 8) take rows j*8 + t and 64 + j*8 + t
+// (j = g % 8) of that head — a rotation pair sits in neighbouring 16-lane
+// segments of one wave and meets through a 32-lane swizzle
 __device__ __forceinline__ int rope_row(int set) {
     const int g = set >> 4, s = set & 15;
-    const int local = (s < 8) ? ((g & 7) * 8 + s) : (64 + (g & 7) * 8 + (s - 8));
-    return (g >> 3) * 128 + local;
+    const int i = (g & 7) * 8 + (s >> 1);
+    return (g >> 3) * 128 + ((s & 1) ? 64 + i : i);
 }
 
 template <int BT, int LPR, int NCH, int RPS, int MODE, int XM, bool LOOP>
@@ -643,7 +645,6 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
         if constexpr (PAIR) acc[0] = silu_mul(acc[0], qwen::swz_xor16_f32(acc[0]));  // gate (even set) x up
         if constexpr (ROPE_EPI) {
             if (p.rope) {  // block-uniform: one pass over 16-row groups of one head
-                __shared__ uint16_t s_rv[16];
                 const int row = rope_row(st);
                 const int u = __builtin_amdgcn_readfirstlane(row & ~127);
                 const int m = (u >= qka.rb1) + (u >= qka.rb2);
@@ -653,16 +654,13 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
                 const bool has_bias = pick3(qka.bias, m) != nullptr;
                 _Float16 v = static_cast<_Float16>(acc[0]);
                 if (has_bias) v = v + __builtin_bit_cast(_Float16, rope_bias);
-                if (l == 0) s_rv[seg] = __builtin_bit_cast(uint16_t, v);
-                __syncthreads();
+                const float y = qwen::swz_xor16_f32(static_cast<float>(v));  // the partner row (segment s ^ 1)
                 if (l == 0) {
                     const int pos = rope_pos;
                     const int e = local & 127, head = local >> 7;
                     uint16_t outv = __builtin_bit_cast(uint16_t, v);
-                    if (m < 2) {  // q and k rows rotate with their partner (segment s ^ 8)
-                        const float y = h2f(s_rv[seg ^ 8]);
+                    if (m < 2)  // q and k rows rotate with their partner
                         outv = f2h(rope_rotate(static_cast<float>(v), y, e < 64, rope_sn, rope_cs));
-                    }
                     pick3(qka.out, m)[local] = outv;
                     if (m > 0) {
                         uint16_t* cache = m == 1 ? p.kcache : p.vcache;
