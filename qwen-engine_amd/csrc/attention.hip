@@ -294,11 +294,15 @@ __device__ __forceinline__ void flash_decode_split(const uint16_t* __restrict__ 
             }
         }
         __syncthreads();
-        if (t < nh * 32) {  // thread (head t/32, dims 4*(t%32)..+3)
-            const int hh = t >> 5, d = 4 * (t & 31);
+        // thread (head t/(32Q), dims 4*((t/Q)%32)..+3, quarter t%Q of the lane groups); the Q
+        // partial sums of an output meet through a DPP quad reduction
+        constexpr int Q = NT >= 128 * HP ? 4 : 1;
+        if (t < nh * 32 * Q) {
+            const int hh = t / (32 * Q), d = 4 * ((t / Q) & 31), qg = t % Q;
             float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-            for (int g = 0; g < NG; ++g) {
+            for (int gi = 0; gi < NG / Q; ++gi) {
+                const int g = qg * (NG / Q) + gi;
                 const float w = s_w[hh][g];
                 const float4 v = *reinterpret_cast<const float4*>(&s_o[g][hh][d]);
                 o.x += w * v.x;
@@ -306,8 +310,16 @@ __device__ __forceinline__ void flash_decode_split(const uint16_t* __restrict__ 
                 o.z += w * v.z;
                 o.w += w * v.w;
             }
-            const size_t row = static_cast<size_t>(qh0 + h0 + hh) * kSplits + split;
-            *reinterpret_cast<float4*>(part_o + row * kHeadDim + d) = o;
+            if constexpr (Q == 4) {
+                o.x = qwen::seg_sum<4>(o.x);
+                o.y = qwen::seg_sum<4>(o.y);
+                o.z = qwen::seg_sum<4>(o.z);
+                o.w = qwen::seg_sum<4>(o.w);
+            }
+            if (qg == 0) {
+                const size_t row = static_cast<size_t>(qh0 + h0 + hh) * kSplits + split;
+                *reinterpret_cast<float4*>(part_o + row * kHeadDim + d) = o;
+            }
         }
     }
     QE_TS(5, false);
