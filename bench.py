@@ -41,6 +41,17 @@ def gemv_bytes(N, K, act="q8", out_n=None):
     return N * K // 2 + N * (K // 128) * 2 + a + (out_n if out_n is not None else N) * 2
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -207,15 +218,34 @@ def main():
     K_steps = max(args.steps, 1)
 
     def run_steps(step_fn):
-        g = graph_of(step_fn, K_steps)
-        for _ in range(max(1, args.warmup // max(1, K_steps))):
-            g.replay()
+        """W untimed warmup steps, then exactly K steps timed (one replay of a
+        K-step graph between hipEvents, synchronized on both sides); ten more
+        replays give the spread of the per-step time."""
+        gk = graph_of(step_fn, K_steps)
+        gk.replay()  # first replay of an instantiated graph carries one-time setup
+        if args.warmup > 0:
+            graph_of(step_fn, args.warmup).replay()
         torch.cuda.synchronize()
-        return time_graph(g, 3) / K_steps
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        gk.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / K_steps
+        spread = []
+        for _ in range(10):
+            e0.record()
+            gk.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            spread.append(e0.elapsed_time(e1) / K_steps)
+        spread.sort()
+        return ms, {"p10_us": round(spread[1] * 1e3, 3), "p50_us": round(spread[5] * 1e3, 3),
+                    "p90_us": round(spread[9] * 1e3, 3)}
 
-    ms_per_step = run_steps(fused_step)
+    ms_per_step, step_spread = run_steps(fused_step)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    ms_ref = run_steps(reference_step)
+    ms_ref, _ = run_steps(reference_step)
 
     result = {
         "metric": "W4A16 GEMV GB/s (% HBM peak); decode tok/s Qwen2.5-1.5B tg256",
@@ -237,7 +267,9 @@ def main():
             "bytes_per_step": step_bytes,
             "hbm_frac": round(value / HBM_PEAK_GBS, 4),
             "weight_copies": L,
-            "timing": "HIP graph of K steps, hipEvents, weights rotated over >= 512 MB",
+            "timing": "the K-step HIP graph replayed once untimed (graph setup), W warmup steps, then one "
+                      "replay of the graph of exactly K steps between hipEvents; weights rotated over >= 512 MB",
+            "step_us_spread_10_more_replays": step_spread,
             "reference_launch_sequence": {
                 "launches_per_step": 7, "us_per_step": round(ms_ref * 1e3, 3),
                 "GB/s": round(ref_step_bytes / (ms_ref * 1e-3) / 1e9, 1)},
@@ -461,7 +493,7 @@ def main():
             "kind": "port",
             "sample": f"{reps} x gate+up SwiGLU GEMV 1536->2x8960 (configs[1]'s largest projection) with the "
                       f"scalar oracle (restated CPU golden, tests/test_kernels.cu:308-363), ~10 s, 1 thread; "
-                      f"host nproc={os.cpu_count()}",
+                      f"host nproc={os.cpu_count()}, CPU {cpu_model()}",
             "all_cores": {"value": round(b_gu * reps_mt / dt_mt / 1e9, 3), "unit": "GB/s", "cores": threads,
                           "sample": f"{reps_mt} x the same GEMV, rows split over {threads} threads, ~5 s"},
         }
