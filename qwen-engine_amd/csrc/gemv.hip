@@ -369,9 +369,12 @@ __device__ __forceinline__ void stage_finish_f16(const GemvParams& p, uint4 (&ra
     // 16-lane row is a whole group, so such rows never mix with real ones)
     // and stores to a dummy LDS slot (s_rec[KC]) when out of range
     const int KC = K >> 5;
+    const int wave_first = __builtin_amdgcn_readfirstlane(t) & ~63;
 #pragma unroll
     for (int j = 0; j < MAXP; ++j) {
-        if (BT * j < U) {  // compile-time for the shapes that use one pass
+        // a wave whose units all lie past the end skips the pass (wave-uniform;
+        // U is a multiple of 16, so a 16-lane group is all real or all past)
+        if (BT * j < U && (j == 0 || wave_first + BT * j < U)) {
             const int u = t + BT * j;
             const bool ok = u < U;
             float vals[8];
