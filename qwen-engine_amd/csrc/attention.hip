@@ -478,38 +478,49 @@ __global__ __launch_bounds__(64 * GROUP) void prefill_attention_mfma_kernel(
     for (int dt = 0; dt < 4; ++dt) acc[dt] = f32x16{};
     float mrow = -INFINITY, lrow = 0.0f;
 
-    // V tile (32 keys x 128 dims) -> LDS as V^T: chunk c = (key c/16, dims 8*(c%16)..+7)
-    auto stage_v = [&](int t0, int buf) __attribute__((always_inline)) {
-        for (int c = threadIdx.x; c < kPkTile * 16; c += NT) {
-            const int key = c >> 4, d0 = 8 * (c & 15);
-            const int pos = min(t0 + key, max_seq - 1);
-            const u32x4 v = *reinterpret_cast<const u32x4*>(vc + hb + static_cast<size_t>(pos) * kHeadDim + d0);
+    // K and V of a tile are requested two tiles ahead: the loop runs over
+    // pairs of tiles with two register slots (an odd tile count ends with a
+    // fully masked tile), so the loads of tile i + 2 are in flight while tile
+    // i computes and every load is unconditional (positions clamped).
+    constexpr int VC = (kPkTile * 16 + NT - 1) / NT;  // V chunks per thread
+    auto load_k = [&](int t0, u32x4 (&kf)[8]) __attribute__((always_inline)) {
+        const int kpos = min(t0 + fr, max_seq - 1);
+        const uint16_t* kr = kc + hb + static_cast<size_t>(kpos) * kHeadDim + 8 * h;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t w = v[e];
-                sVt[buf][(d0 + 2 * e) * kVtStride + key] = static_cast<uint16_t>(w & 0xFFFFu);
-                sVt[buf][(d0 + 2 * e + 1) * kVtStride + key] = static_cast<uint16_t>(w >> 16);
+        for (int kk = 0; kk < 8; ++kk) kf[kk] = *reinterpret_cast<const u32x4*>(kr + 16 * kk);
+    };
+    // V tile (32 keys x 128 dims), chunk c = (key c/16, dims 8*(c%16)..+7)
+    auto load_v = [&](int t0, u32x4 (&vr)[VC]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < VC; ++i) {
+            const int c = min(static_cast<int>(threadIdx.x) + NT * i, kPkTile * 16 - 1);
+            const int pos = min(t0 + (c >> 4), max_seq - 1);
+            vr[i] = *reinterpret_cast<const u32x4*>(vc + hb + static_cast<size_t>(pos) * kHeadDim + 8 * (c & 15));
+        }
+    };
+    // -> LDS as V^T
+    auto store_v = [&](const u32x4 (&vr)[VC], int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < VC; ++i) {
+            const int c = static_cast<int>(threadIdx.x) + NT * i;
+            if (c < kPkTile * 16) {
+                const int key = c >> 4, d0 = 8 * (c & 15);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t w = vr[i][e];
+                    sVt[buf][(d0 + 2 * e) * kVtStride + key] = static_cast<uint16_t>(w & 0xFFFFu);
+                    sVt[buf][(d0 + 2 * e + 1) * kVtStride + key] = static_cast<uint16_t>(w >> 16);
+                }
             }
         }
     };
-    stage_v(0, 0);
-    __syncthreads();
-    int buf = 0;
-    for (int t0 = 0; t0 < kv_len; t0 += kPkTile) {
-        // S^T = K . Q^T
+    // one tile: S^T = K . Q^T, online softmax, O^T += V^T . P^T (V^T in sVt[buf])
+    auto tile = [&](int t0, const u32x4 (&kf)[8], int buf) __attribute__((always_inline)) {
         f32x16 sacc = f32x16{};
-        {
-            const int kpos = min(t0 + fr, max_seq - 1);
-            const uint16_t* kr = kc + hb + static_cast<size_t>(kpos) * kHeadDim + 8 * h;
-            u32x4 kf[8];
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) kf[kk] = *reinterpret_cast<const u32x4*>(kr + 16 * kk);
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk)
-                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf[kk]),
-                                                              __builtin_bit_cast(f16x8, qf[kk]), sacc, 0, 0, 0);
-        }
-        if (t0 + kPkTile < kv_len) stage_v(t0 + kPkTile, buf ^ 1);  // next tile, other buffer
+        for (int kk = 0; kk < 8; ++kk)
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf[kk]),
+                                                          __builtin_bit_cast(f16x8, qf[kk]), sacc, 0, 0, 0);
         // online softmax over this lane's 16 keys (+ the partner lane's 16)
         float sv[16];
         float mx = -INFINITY;
@@ -538,7 +549,7 @@ __global__ __launch_bounds__(64 * GROUP) void prefill_attention_mfma_kernel(
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[dt][v] *= alpha;
-        // O^T += V^T . P^T, two 16-key halves of the tile
+        // two 16-key halves of the tile
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const u32x4 pf = {pw[4 * ks], pw[4 * ks + 1], pw[4 * ks + 2], pw[4 * ks + 3]};
@@ -552,8 +563,25 @@ __global__ __launch_bounds__(64 * GROUP) void prefill_attention_mfma_kernel(
                                                                  __builtin_bit_cast(f16x8, pf), acc[dt], 0, 0, 0);
             }
         }
-        __syncthreads();  // this tile's V^T is consumed; the next one is stored
-        buf ^= 1;
+    };
+    u32x4 k0[8], k1[8], v0[VC], v1[VC];
+    load_k(0, k0);
+    load_v(0, v0);
+    load_k(kPkTile, k1);
+    load_v(kPkTile, v1);
+    store_v(v0, 0);
+    __syncthreads();
+    for (int t0 = 0; t0 < kv_len; t0 += 2 * kPkTile) {
+        load_v(t0 + 2 * kPkTile, v0);  // sVt[0] holds tile t0; v0 is free
+        tile(t0, k0, 0);
+        load_k(t0 + 2 * kPkTile, k0);
+        store_v(v1, 1);  // tile t0 + 32, requested one tile ago
+        __syncthreads();
+        load_v(t0 + 3 * kPkTile, v1);
+        tile(t0 + kPkTile, k1, 1);
+        load_k(t0 + 3 * kPkTile, k1);
+        store_v(v0, 0);  // tile t0 + 64
+        __syncthreads();
     }
     lrow += __shfl_xor(lrow, 32);
     if (m < T) {

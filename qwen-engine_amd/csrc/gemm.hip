@@ -64,42 +64,46 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f +
 constexpr size_t kWsFloats = size_t(8) << 20;  // 32 MiB
 __device__ float g_splitk_ws[kWsFloats];
 
+// One 32x32 accumulator fragment whose rows start at r0 and whose lane
+// column is col.  D[i][j] of a 32x32 MFMA tile: j = lane%32,
+// i = 8*(v/4) + 4*(lane/32) + v%4
+template <int MODE>
+__device__ __forceinline__ void epilogue_frag(const GemmParams& p, const f32x16& acc, int r0, int col, int lane) {
+    const int fr = lane & 31;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int row = r0 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const float a = acc[v];
+        if constexpr (MODE == kSwiglu) {
+            const float partner = __shfl_xor(a, 1);
+            if ((fr & 1) == 0 && row < p.M && col < p.N)
+                p.out[0][static_cast<size_t>(row) * p.out_stride[0] + (col >> 1)] = f2h(silu_mul(a, partner));
+        } else {
+            if (row < p.M && col < p.N) {
+                int m = 0, local = col;
+                if constexpr (MODE == kQKV) {
+                    m = (col >= p.col_begin[1]) + (col >= p.col_begin[2]);
+                    local = col - p.col_begin[m];
+                }
+                const size_t off = static_cast<size_t>(row) * p.out_stride[m] + local;
+                _Float16 h = static_cast<_Float16>(a);
+                if (MODE == kPlain && p.residual != nullptr)
+                    h = h + __builtin_bit_cast(_Float16, p.residual[off]);  // fp16 add, RNE
+                p.out[m][off] = __builtin_bit_cast(uint16_t, h);
+            }
+        }
+    }
+}
+
 template <int BM, int BN, int WGM, int MODE>
 __device__ __forceinline__ void epilogue(const GemmParams& p, const f32x16 (&acc)[BM / WGM / 32][BN / (4 / WGM) / 32],
                                          int m0, int n0, int wm, int wn, int lane) {
     constexpr int WM = BM / WGM, WN = BN / (4 / WGM), MI = WM / 32, NI = WN / 32;
-    const int fr = lane & 31;
-    // D[i][j] of a 32x32 MFMA tile: j = lane%32, i = 8*(v/4) + 4*(lane/32) + v%4
 #pragma unroll
-    for (int i = 0; i < MI; ++i) {
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < NI; ++j) {
-            const int col = n0 + wn * WN + j * 32 + fr;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                const float a = acc[i][j][v];
-                if constexpr (MODE == kSwiglu) {
-                    const float partner = __shfl_xor(a, 1);
-                    if ((fr & 1) == 0 && row < p.M && col < p.N)
-                        p.out[0][static_cast<size_t>(row) * p.out_stride[0] + (col >> 1)] = f2h(silu_mul(a, partner));
-                } else {
-                    if (row < p.M && col < p.N) {
-                        int m = 0, local = col;
-                        if constexpr (MODE == kQKV) {
-                            m = (col >= p.col_begin[1]) + (col >= p.col_begin[2]);
-                            local = col - p.col_begin[m];
-                        }
-                        const size_t off = static_cast<size_t>(row) * p.out_stride[m] + local;
-                        _Float16 h = static_cast<_Float16>(a);
-                        if (MODE == kPlain && p.residual != nullptr)
-                            h = h + __builtin_bit_cast(_Float16, p.residual[off]);  // fp16 add, RNE
-                        p.out[m][off] = __builtin_bit_cast(uint16_t, h);
-                    }
-                }
-            }
-        }
-    }
+        for (int j = 0; j < NI; ++j)
+            epilogue_frag<MODE>(p, acc[i][j], m0 + wm * WM + i * 32, n0 + wn * WN + j * 32 + (lane & 31), lane);
 }
 
 // Block tile BM x BN, 4 waves in a WGM x (4/WGM) grid, wave tile WM x WN of
@@ -290,30 +294,54 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
             for (int v = 0; v < 16; ++v) mine[((i * NI + j) * 16 + v) * 256 + tid] = acc[i][j][v];
 }
 
-// Sums the K-slice partials of each tile in slice order and applies the
-// epilogue.  grid (N tiles, M tiles), 256 threads (the MFMA lane layout).
-template <int BM, int BN, int WGM, int MODE>
+// Sums the K-slice partials in slice order and applies the epilogue.  grid
+// (N tiles, M tiles, fragments): block z takes the 32x32 fragment z of its
+// tile, 256 threads in the MFMA lane layout of the 4 waves.  S > 0: all S
+// slices are requested before the first add (one memory latency, not S);
+// S = 0: a loop over the slices.
+template <int BM, int BN, int WGM, int MODE, int S>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, int slices) {
     constexpr int WGN = 4 / WGM;
-    constexpr int MI = BM / WGM / 32, NI = BN / WGN / 32;
+    constexpr int WM = BM / WGM, WN = BN / WGN, NI = WN / 32;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile = blockIdx.y * gridDim.x + blockIdx.x;
     const int n_tiles = gridDim.x * gridDim.y;
-    f32x16 acc[MI][NI];
+    const int f = blockIdx.z, i = f / NI, j = f % NI;
+    const size_t slice_stride = static_cast<size_t>(n_tiles) * (BM * BN);
+    const float* part = g_splitk_ws + static_cast<size_t>(tile) * (BM * BN) + f * 16 * 256 + tid;
+    f32x16 acc = f32x16{};
+    if constexpr (S > 0) {
+        float x[S][16];
 #pragma unroll
-    for (int i = 0; i < MI; ++i)
+        for (int z = 0; z < S; ++z)
 #pragma unroll
-        for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
-    for (int z = 0; z < slices; ++z) {
-        const float* part = g_splitk_ws + (static_cast<size_t>(z) * n_tiles + tile) * (BM * BN);
+            for (int v = 0; v < 16; ++v) x[z][v] = part[z * slice_stride + v * 256];
 #pragma unroll
-        for (int i = 0; i < MI; ++i)
+        for (int z = 0; z < S; ++z)
 #pragma unroll
-            for (int j = 0; j < NI; ++j)
+            for (int v = 0; v < 16; ++v) acc[v] += x[z][v];
+    } else {
+        for (int z = 0; z < slices; ++z)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) acc[i][j][v] += part[((i * NI + j) * 16 + v) * 256 + tid];
+            for (int v = 0; v < 16; ++v) acc[v] += part[z * slice_stride + v * 256];
     }
-    epilogue<BM, BN, WGM, MODE>(p, acc, blockIdx.y * BM, blockIdx.x * BN, wave / WGN, wave % WGN, lane);
+    const int wm = wave / WGN, wn = wave % WGN;
+    epilogue_frag<MODE>(p, acc, blockIdx.y * BM + wm * WM + i * 32, blockIdx.x * BN + wn * WN + j * 32 + (lane & 31),
+                        lane);
+}
+
+template <int BM, int BN, int WGM, int MODE>
+void launch_reduce(const GemmParams& p, dim3 tiles, int slices, hipStream_t s) {
+    constexpr int FR = (BM / WGM / 32) * (BN / (4 / WGM) / 32);  // fragments per wave
+    const dim3 grid(tiles.x, tiles.y, FR);
+    switch (slices) {
+        case 2: gemm_splitk_reduce_kernel<BM, BN, WGM, MODE, 2><<<grid, 256, 0, s>>>(p, slices); break;
+        case 3: gemm_splitk_reduce_kernel<BM, BN, WGM, MODE, 3><<<grid, 256, 0, s>>>(p, slices); break;
+        case 4: gemm_splitk_reduce_kernel<BM, BN, WGM, MODE, 4><<<grid, 256, 0, s>>>(p, slices); break;
+        case 6: gemm_splitk_reduce_kernel<BM, BN, WGM, MODE, 6><<<grid, 256, 0, s>>>(p, slices); break;
+        case 8: gemm_splitk_reduce_kernel<BM, BN, WGM, MODE, 8><<<grid, 256, 0, s>>>(p, slices); break;
+        default: gemm_splitk_reduce_kernel<BM, BN, WGM, MODE, 0><<<grid, 256, 0, s>>>(p, slices); break;
+    }
 }
 
 template <int BM, int BN, int WGM, int MODE>
@@ -323,7 +351,7 @@ void launch_tiles(const GemmParams& p, int slices, hipStream_t s) {
         gemm_w4a16_mfma_kernel<BM, BN, WGM, MODE, true><<<grid, 256, 0, s>>>(p);
     else
         gemm_w4a16_mfma_kernel<BM, BN, WGM, MODE, false><<<grid, 256, 0, s>>>(p);
-    if (slices > 1) gemm_splitk_reduce_kernel<BM, BN, WGM, MODE><<<dim3(grid.x, grid.y), 256, 0, s>>>(p, slices);
+    if (slices > 1) launch_reduce<BM, BN, WGM, MODE>(p, grid, slices, s);
 }
 
 // Launch-time model of one configuration (tile, K slices), in microseconds,
@@ -560,8 +588,8 @@ int launch_gemm_w4a8(const GemmParams& p, hipStream_t stream, const char* what) 
     if (big) gemm_w4a8_mfma_kernel<128, MODE><<<g3, 256, 0, stream>>>(p);
     else gemm_w4a8_mfma_kernel<64, MODE><<<g3, 256, 0, stream>>>(p);
     if (slices > 1) {
-        if (big) gemm_splitk_reduce_kernel<128, 128, 1, MODE><<<grid, 256, 0, stream>>>(p, slices);
-        else gemm_splitk_reduce_kernel<64, 128, 1, MODE><<<grid, 256, 0, stream>>>(p, slices);
+        if (big) launch_reduce<128, 128, 1, MODE>(p, grid, slices, stream);
+        else launch_reduce<64, 128, 1, MODE>(p, grid, slices, stream);
     }
     return check_launch(what);
 }
