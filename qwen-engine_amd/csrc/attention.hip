@@ -428,8 +428,9 @@ __global__ __launch_bounds__(128) void flash_decode_stage2_kernel(const float* _
 }
 
 // ---- causal prefill attention (matrix cores) ---------------------------------------
-// grid (num_kv_heads, ceil(T/32)), GROUP waves: wave w is q head kvh*GROUP + w,
-// the block's 32 queries are m0..m0+31 (position base + m; keys [0, base + m]).
+// grid (num_q_heads / WPB, ceil(T/32)), WPB waves: wave w is q head
+// blockIdx.x*WPB + w (the WPB heads of a block share one kv head), the block's
+// 32 queries are m0..m0+31 (position base + m; keys [0, base + m]).
 // v_mfma_f32_32x32x16_f16 with queries as the columns:
 //   S^T (32 keys x 32 queries) = K (keys x 128 dims) . Q^T — lane l holds key
 //   row l%32 / query column l%32, dims 8*(l/32) + 16*kk: one 16-byte load each
@@ -439,29 +440,35 @@ __global__ __launch_bounds__(128) void flash_decode_stage2_kernel(const float* _
 //   O^T (128 dims x 32 queries) += V^T . P^T — P^T is the lane's own 16
 //   probabilities (fp16, k order = the keys it holds; the k order inside an
 //   MFMA is free when both operands agree) and V^T comes from an LDS tile the
-//   block stores transposed (two 8-byte reads per MFMA).
-// Online softmax in the exp2 domain, fp32 accumulation; the output is O / L.
+//   block stores transposed as key pairs (one 32-bit word = two keys of one
+//   dim; rows of 18 words: conflict-free stores and 8-byte reads).
+// Online softmax in the exp2 domain (the 1/sqrt(d) scale folded into the
+// exponent's fused multiply-add), fp32 accumulation; the output is O / L.
+// Tiles wholly below the diagonal and inside the context skip the mask; the
+// accumulator rescale is skipped when no lane's running max moved.
 constexpr int kPqTile = 32;      // queries per block
 constexpr int kPkTile = 32;      // keys per step
-constexpr int kVtStride = 40;    // halves per LDS row of V^T (32 keys + 8 pad)
+constexpr int kVtWords = 18;     // 32-bit words per LDS row of V^T (16 key pairs + 2 pad)
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int GROUP>
-__global__ __launch_bounds__(64 * GROUP) void prefill_attention_mfma_kernel(
+template <int WPB>
+__global__ __launch_bounds__(64 * WPB) void prefill_attention_mfma_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
-    uint16_t* __restrict__ out, const qe_device_control_block* ctl, int T, int nq, int max_seq, int out_stride) {
-    constexpr int NT = 64 * GROUP;
-    __shared__ __align__(16) uint16_t sVt[2][kHeadDim * kVtStride];
-    const int kvh = blockIdx.x, m0 = blockIdx.y * kPqTile;
+    uint16_t* __restrict__ out, const qe_device_control_block* ctl, int T, int nq, int group, int max_seq,
+    int out_stride) {
+    constexpr int NT = 64 * WPB;
+    __shared__ __align__(16) uint32_t sVt[2][kHeadDim * kVtWords];
+    const int qh0 = blockIdx.x * WPB, kvh = qh0 / group, m0 = blockIdx.y * kPqTile;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int qh = kvh * GROUP + wave;
+    const int qh = qh0 + wave;
     const int fr = lane & 31, h = lane >> 5;
     const int base = ctl != nullptr ? ctl->seq_pos : 0;
     const int m = m0 + fr;                       // this lane's query
     const int qpos = base + m;                    // its position
     const int last = min(m0 + kPqTile - 1, T - 1);
     const int kv_len = min(base + last + 1, max_seq);
+    const int first_diag = base + m0;             // keys below this are visible to every query of the block
     const size_t hb = static_cast<size_t>(kvh) * max_seq * kHeadDim;
     constexpr float kScale = 1.4426950408889634f * 0.08838834764831845f;  // log2(e) / sqrt(128)
 
@@ -482,34 +489,38 @@ __global__ __launch_bounds__(64 * GROUP) void prefill_attention_mfma_kernel(
     // pairs of tiles with two register slots (an odd tile count ends with a
     // fully masked tile), so the loads of tile i + 2 are in flight while tile
     // i computes and every load is unconditional (positions clamped).
-    constexpr int VC = (kPkTile * 16 + NT - 1) / NT;  // V chunks per thread
+    constexpr int VC = (kPkTile / 2 * 16 + NT - 1) / NT;  // (key pair, 8 dims) chunks per thread
     auto load_k = [&](int t0, u32x4 (&kf)[8]) __attribute__((always_inline)) {
         const int kpos = min(t0 + fr, max_seq - 1);
         const uint16_t* kr = kc + hb + static_cast<size_t>(kpos) * kHeadDim + 8 * h;
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) kf[kk] = *reinterpret_cast<const u32x4*>(kr + 16 * kk);
     };
-    // V tile (32 keys x 128 dims), chunk c = (key c/16, dims 8*(c%16)..+7)
-    auto load_v = [&](int t0, u32x4 (&vr)[VC]) __attribute__((always_inline)) {
+    // chunk c: key pair c%16 (keys 2(c%16), +1), dims 8*(c/16)..+7
+    auto load_v = [&](int t0, u32x4 (&vr)[VC][2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < VC; ++i) {
-            const int c = min(static_cast<int>(threadIdx.x) + NT * i, kPkTile * 16 - 1);
-            const int pos = min(t0 + (c >> 4), max_seq - 1);
-            vr[i] = *reinterpret_cast<const u32x4*>(vc + hb + static_cast<size_t>(pos) * kHeadDim + 8 * (c & 15));
+            const int c = min(static_cast<int>(threadIdx.x) + NT * i, kPkTile / 2 * 16 - 1);
+            const int kp = c & 15, d0 = 8 * (c >> 4);
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int pos = min(t0 + 2 * kp + r, max_seq - 1);
+                vr[i][r] = *reinterpret_cast<const u32x4*>(vc + hb + static_cast<size_t>(pos) * kHeadDim + d0);
+            }
         }
     };
-    // -> LDS as V^T
-    auto store_v = [&](const u32x4 (&vr)[VC], int buf) __attribute__((always_inline)) {
+    // -> LDS as V^T key pairs: word (dim d, pair kp) = V[2kp][d] | V[2kp+1][d] << 16
+    auto store_v = [&](const u32x4 (&vr)[VC][2], int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < VC; ++i) {
             const int c = static_cast<int>(threadIdx.x) + NT * i;
-            if (c < kPkTile * 16) {
-                const int key = c >> 4, d0 = 8 * (c & 15);
+            if (c < kPkTile / 2 * 16) {
+                const int kp = c & 15, d0 = 8 * (c >> 4);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const uint32_t w = vr[i][e];
-                    sVt[buf][(d0 + 2 * e) * kVtStride + key] = static_cast<uint16_t>(w & 0xFFFFu);
-                    sVt[buf][(d0 + 2 * e + 1) * kVtStride + key] = static_cast<uint16_t>(w >> 16);
+                    const uint32_t a = vr[i][0][e], b = vr[i][1][e];  // dims d0+2e (low half), d0+2e+1
+                    sVt[buf][(d0 + 2 * e) * kVtWords + kp] = __builtin_amdgcn_perm(b, a, 0x05040100u);
+                    sVt[buf][(d0 + 2 * e + 1) * kVtWords + kp] = __builtin_amdgcn_perm(b, a, 0x07060302u);
                 }
             }
         }
@@ -521,50 +532,58 @@ __global__ __launch_bounds__(64 * GROUP) void prefill_attention_mfma_kernel(
         for (int kk = 0; kk < 8; ++kk)
             sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf[kk]),
                                                           __builtin_bit_cast(f16x8, qf[kk]), sacc, 0, 0, 0);
-        // online softmax over this lane's 16 keys (+ the partner lane's 16)
+        // raw scores of this lane's 16 keys; masked ones -inf
         float sv[16];
+        if (t0 + kPkTile > first_diag || t0 + kPkTile > kv_len) {  // block-uniform
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int key = t0 + 8 * (v >> 2) + 4 * h + (v & 3);
+                sv[v] = (key < kv_len && key <= qpos && m < T) ? sacc[v] : -INFINITY;
+            }
+        } else {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sv[v] = sacc[v];
+        }
         float mx = -INFINITY;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int key = t0 + 8 * (v >> 2) + 4 * h + (v & 3);
-            const bool ok = key < kv_len && key <= qpos && m < T;
-            sv[v] = ok ? sacc[v] * kScale : -INFINITY;
-            mx = fmaxf(mx, sv[v]);
-        }
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sv[v]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mn = fmaxf(mrow, mx);
+        const float mn = fmaxf(mrow, mx * kScale);  // scaling is monotonic: max of the scaled scores
         const float alpha = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mrow - mn);
         mrow = mn;
+        const float neg = mn == -INFINITY ? 0.0f : -mn;  // masked scores give exp2(-inf) = 0
         float ps = 0.0f;
         uint32_t pw[8];
 #pragma unroll
         for (int v = 0; v < 16; v += 2) {
-            const float p0 = sv[v] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[v] - mn);
-            const float p1 = sv[v + 1] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[v + 1] - mn);
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[v], kScale, neg));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[v + 1], kScale, neg));
             ps += p0 + p1;
             pw[v >> 1] = static_cast<uint32_t>(f2h(p0)) | (static_cast<uint32_t>(f2h(p1)) << 16);
         }
         lrow = lrow * alpha + ps;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
+            for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[dt][v] *= alpha;
+                for (int v = 0; v < 16; ++v) acc[dt][v] *= alpha;
+        }
         // two 16-key halves of the tile
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const u32x4 pf = {pw[4 * ks], pw[4 * ks + 1], pw[4 * ks + 2], pw[4 * ks + 3]};
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const uint16_t* row = &sVt[buf][(32 * dt + fr) * kVtStride + 16 * ks + 4 * h];
+                const uint32_t* row = &sVt[buf][(32 * dt + fr) * kVtWords + 8 * ks + 2 * h];
                 const uint2 lo = *reinterpret_cast<const uint2*>(row);      // keys 16ks + 4h .. +3
-                const uint2 hi = *reinterpret_cast<const uint2*>(row + 8);  // keys 16ks + 8 + 4h .. +3
+                const uint2 hi = *reinterpret_cast<const uint2*>(row + 4);  // keys 16ks + 8 + 4h .. +3
                 const u32x4 vf = {lo.x, lo.y, hi.x, hi.y};
                 acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf),
                                                                  __builtin_bit_cast(f16x8, pf), acc[dt], 0, 0, 0);
             }
         }
     };
-    u32x4 k0[8], k1[8], v0[VC], v1[VC];
+    u32x4 k0[8], k1[8], v0[VC][2], v1[VC][2];
     load_k(0, k0);
     load_v(0, v0);
     load_k(kPkTile, k1);
@@ -724,14 +743,17 @@ extern "C" int qe_launch_attention_gqa_prefill(const uint16_t* q, const uint16_t
     QE_REQUIRE(aligned(q, 16) && aligned(attn_out, 8) && hidden_size % 4 == 0,
                "attention_gqa_prefill: q must be 16-byte and attn_out 8-byte aligned");
     const int group = num_q_heads / num_kv_heads;
-    const dim3 grid(num_kv_heads, (num_tokens + kPqTile - 1) / kPqTile);
-    switch (group) {
-        case 1: prefill_attention_mfma_kernel<1><<<grid, 64, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, num_q_heads, max_seq_len, hidden_size); break;
-        case 2: prefill_attention_mfma_kernel<2><<<grid, 128, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, num_q_heads, max_seq_len, hidden_size); break;
-        case 4: prefill_attention_mfma_kernel<4><<<grid, 256, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, num_q_heads, max_seq_len, hidden_size); break;
-        case 6: prefill_attention_mfma_kernel<6><<<grid, 384, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, num_q_heads, max_seq_len, hidden_size); break;
-        case 8: prefill_attention_mfma_kernel<8><<<grid, 512, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control, num_tokens, num_q_heads, max_seq_len, hidden_size); break;
-        default: return fail(QE_ERR_UNSUPPORTED, "attention_gqa_prefill: %d q heads per kv head (built: 1, 2, 4, 6, 8)", group);
-    }
+    // two q heads per block when the group splits evenly (one wave per SIMD,
+    // group/2 blocks per kv head and query tile), else one
+    const int wpb = group % 2 == 0 ? 2 : 1;
+    const dim3 grid(num_q_heads / wpb, (num_tokens + kPqTile - 1) / kPqTile);
+    if (wpb == 2)
+        prefill_attention_mfma_kernel<2><<<grid, 128, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control,
+                                                                   num_tokens, num_q_heads, group, max_seq_len,
+                                                                   hidden_size);
+    else
+        prefill_attention_mfma_kernel<1><<<grid, 64, 0, stream>>>(q, layer_k_cache, layer_v_cache, attn_out, d_control,
+                                                                  num_tokens, num_q_heads, group, max_seq_len,
+                                                                  hidden_size);
     return check_launch("attention_gqa_prefill");
 }

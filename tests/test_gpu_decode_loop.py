@@ -201,7 +201,7 @@ def test_qkv_bias_rope_kv_append(qe):
 
 @pytest.mark.parametrize("T,base,nq,nkv", [(1, 0, 12, 2), (37, 0, 12, 2), (128, 0, 12, 2), (20, 100, 12, 2),
                                            (33, 31, 12, 2), (200, 300, 12, 2), (70, 5, 8, 1), (45, 0, 4, 4),
-                                           (64, 17, 4, 2)])
+                                           (64, 17, 4, 2), (300, 0, 12, 2), (96, 10, 15, 5), (60, 452, 12, 2)])
 def test_prefill_attention(qe, T, base, nq, nkv):
     D, max_seq = 128, 512
     rng = np.random.default_rng(T + base)
