@@ -70,15 +70,27 @@ __device__ float g_splitk_ws[kWsFloats];
 template <int MODE>
 __device__ __forceinline__ void epilogue_frag(const GemmParams& p, const f32x16& acc, int r0, int col, int lane) {
     const int fr = lane & 31;
+    auto row_of = [&](int v) __attribute__((always_inline)) { return r0 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); };
+    if constexpr (MODE == kSwiglu) {
+        // lane pair (gate column, up column): the gate lane finishes rows
+        // v < 8 and the up lane rows v >= 8, so every lane evaluates 8 silu
+        const bool gate = (fr & 1) == 0;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const float recv = __shfl_xor(gate ? acc[v + 8] : acc[v], 1);
+            const float g = gate ? acc[v] : recv;
+            const float u = gate ? recv : acc[v + 8];
+            const int row = row_of(gate ? v : v + 8);
+            if (row < p.M && col < p.N)
+                p.out[0][static_cast<size_t>(row) * p.out_stride[0] + (col >> 1)] = f2h(silu_mul(g, u));
+        }
+        return;
+    }
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-        const int row = r0 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const int row = row_of(v);
         const float a = acc[v];
-        if constexpr (MODE == kSwiglu) {
-            const float partner = __shfl_xor(a, 1);
-            if ((fr & 1) == 0 && row < p.M && col < p.N)
-                p.out[0][static_cast<size_t>(row) * p.out_stride[0] + (col >> 1)] = f2h(silu_mul(a, partner));
-        } else {
+        {
             if (row < p.M && col < p.N) {
                 int m = 0, local = col;
                 if constexpr (MODE == kQKV) {
