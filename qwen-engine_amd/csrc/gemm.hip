@@ -224,13 +224,21 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
 
-#pragma unroll
-    for (int d = 0; d < D; ++d) load_a(min(d, KT - 1), d);
+    // prologue loads in the order of the steady state (QUAD: the quad's
+    // weights, then the A ring; else A and weights step by step): the wait at
+    // the loop head is sized for both the entry and the back edge, so an
+    // entry that issued the weights last would make every iteration drain
+    // its loads there
     if constexpr (QUAD) {
         load_b(0, 0);
+#pragma unroll
+        for (int d = 0; d < D; ++d) load_a(min(d, KT - 1), d);
     } else {
 #pragma unroll
-        for (int d = 0; d < D; ++d) load_b(min(d, KT - 1), d);
+        for (int d = 0; d < D; ++d) {
+            load_a(min(d, KT - 1), d);
+            load_b(min(d, KT - 1), d);
+        }
     }
     store_a(0, 0);
     __syncthreads();
