@@ -93,10 +93,13 @@ __device__ __forceinline__ Q8Group quantize_group128_q8_1(const float vals[8]) {
     for (int j = 0; j < 8; ++j) {
         // roundf (half away from zero) as trunc(y + copysign(0.5 - 2^-25, y)):
         // equal to roundf for every |y| < 2^23 (checked exhaustively on the
-        // host); the product is rounded on its own, never fused into the add
+        // host); the product is rounded on its own, never fused into the add.
+        // No clamp to +-127 is needed: |vals[j]| <= max_abs and rounding is
+        // monotonic, and max_abs * inv_d rounds to at most 127 for every
+        // positive finite max_abs (checked exhaustively on the host); NaN
+        // converts to 0 as before.
         const float y = vals[j] * inv_d;
-        int v = static_cast<int>(y + __builtin_copysignf(0.49999997f, y));
-        v = max(-127, min(127, v));
+        const int v = static_cast<int>(y + __builtin_copysignf(0.49999997f, y));
         b[j] = static_cast<uint32_t>(v) & 0xFFu;
     }
     Q8Group g;
