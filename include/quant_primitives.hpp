@@ -50,6 +50,20 @@ __device__ __forceinline__ float seg_max(float v) {
     return v;
 }
 
+// Max over aligned groups of SEG <= 16 lanes of values that are >= +0 and
+// not NaN: their bit patterns order as unsigned integers, so each step is one
+// DPP-fused integer max (no NaN canonicalization).
+template <int SEG>
+__device__ __forceinline__ float seg_max_nonneg(float v) {
+    static_assert(SEG <= 16, "DPP row");
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    if constexpr (SEG >= 2) u = max(u, static_cast<uint32_t>(dpp_i32<0xB1>(static_cast<int>(u))));
+    if constexpr (SEG >= 4) u = max(u, static_cast<uint32_t>(dpp_i32<0x4E>(static_cast<int>(u))));
+    if constexpr (SEG >= 8) u = max(u, static_cast<uint32_t>(dpp_i32<0x141>(static_cast<int>(u))));
+    if constexpr (SEG >= 16) u = max(u, static_cast<uint32_t>(dpp_i32<0x140>(static_cast<int>(u))));
+    return __builtin_bit_cast(float, u);
+}
+
 // ---- integer dot primitives ---------------------------------------------
 // compute_q8_sum8 (reference quant_primitives.cuh:13-17): -8 * sum of the
 // 8 signed bytes of (x_lo, x_hi).
@@ -85,7 +99,7 @@ __device__ __forceinline__ Q8Group quantize_group128_q8_1(const float vals[8]) {
     float max_abs = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) max_abs = fmaxf(max_abs, fabsf(vals[j]));
-    max_abs = seg_max<16>(max_abs);
+    max_abs = seg_max_nonneg<16>(max_abs);  // fmaxf from +0 never yields NaN or -0
     float d = fmaxf(max_abs / 127.0f, 1e-8f);
     float inv_d = 1.0f / d;
     uint32_t b[8];

@@ -462,7 +462,7 @@ __device__ __forceinline__ void stage_finish_attn(const GemvParams& p, const flo
             hw[j] = static_cast<uint32_t>(f2h(acc[2 * j])) | (static_cast<uint32_t>(f2h(acc[2 * j + 1])) << 16);
         *reinterpret_cast<uint4*>(p.norm_out + 8 * u) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     }
-    const float d = flash_q8_scale(qwen::seg_max<16>(mx));
+    const float d = flash_q8_scale(qwen::seg_max_nonneg<16>(mx));  // mx: fmaxf from +0, never NaN
     uint32_t b[8];
     int qsum = 0;
 #pragma unroll
