@@ -53,7 +53,11 @@ struct GemmParams {
     int M, N, K;       // N = virtual columns (SwiGLU: 2*I)
 };
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+// silu(g) * u = g * u / (1 + e^-g) with the hardware exp2 and reciprocal
+// (about 1 ulp each in fp32; the result is rounded to fp16)
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return g * u * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.44269504088896341f * g));
+}
 
 // Split-K scratch: fp32 partial tiles of the K slices, reduced by a second
 // kernel on the same stream (deterministic order, no atomics or fences).  A
@@ -67,42 +71,55 @@ __device__ float g_splitk_ws[kWsFloats];
 // One 32x32 accumulator fragment whose rows start at r0 and whose lane
 // column is col.  D[i][j] of a 32x32 MFMA tile: j = lane%32,
 // i = 8*(v/4) + 4*(lane/32) + v%4
+// Value of the neighbouring lane (lane ^ 1), by DPP within the quad.
+__device__ __forceinline__ float swap_adjacent(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+}
+
 template <int MODE>
 __device__ __forceinline__ void epilogue_frag(const GemmParams& p, const f32x16& acc, int r0, int col, int lane) {
     const int fr = lane & 31;
-    auto row_of = [&](int v) __attribute__((always_inline)) { return r0 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); };
+    // rows of element v: r0 + 8 * (v / 4) + 4 * (lane / 32) + v % 4 (static
+    // offsets from the lane's first row; every index into acc is static)
+    const int lrow = r0 + 4 * (lane >> 5);
+    const bool cols_ok = col < p.N;
+    const bool rows_ok = r0 + 32 <= p.M;  // the whole fragment: no per-row checks
     if constexpr (MODE == kSwiglu) {
         // lane pair (gate column, up column): the gate lane finishes rows
-        // v < 8 and the up lane rows v >= 8, so every lane evaluates 8 silu
+        // v < 8 and the up lane rows v >= 8 (16 further down), so every lane
+        // evaluates 8 silu; the partner's values arrive by DPP swaps
         const bool gate = (fr & 1) == 0;
+        const int row0 = lrow + (gate ? 0 : 16);
+        const int stride = p.out_stride[0];
+        uint16_t* out = p.out[0] + (col >> 1);
 #pragma unroll
         for (int v = 0; v < 8; ++v) {
-            const float recv = __shfl_xor(gate ? acc[v + 8] : acc[v], 1);
-            const float g = gate ? acc[v] : recv;
-            const float u = gate ? recv : acc[v + 8];
-            const int row = row_of(gate ? v : v + 8);
-            if (row < p.M && col < p.N)
-                p.out[0][static_cast<size_t>(row) * p.out_stride[0] + (col >> 1)] = f2h(silu_mul(g, u));
+            const float lo = acc[v], hi = acc[v + 8];
+            const float lo_x = swap_adjacent(lo), hi_x = swap_adjacent(hi);
+            const float g = gate ? lo : hi_x;
+            const float u = gate ? lo_x : hi;
+            const int row = row0 + 8 * (v >> 2) + (v & 3);
+            if (cols_ok && (rows_ok || row < p.M)) out[static_cast<size_t>(row) * stride] = f2h(silu_mul(g, u));
         }
         return;
     }
+    int m = 0, local = col;
+    if constexpr (MODE == kQKV) {
+        m = (col >= p.col_begin[1]) + (col >= p.col_begin[2]);
+        local = col - p.col_begin[m];
+    }
+    const int stride = MODE == kQKV ? (m == 0 ? p.out_stride[0] : m == 1 ? p.out_stride[1] : p.out_stride[2])
+                                    : p.out_stride[0];
+    uint16_t* out = (MODE == kQKV ? (m == 0 ? p.out[0] : m == 1 ? p.out[1] : p.out[2]) : p.out[0]) + local;
+    const uint16_t* res = (MODE == kPlain && p.residual != nullptr) ? p.residual + local : nullptr;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-        const int row = row_of(v);
-        const float a = acc[v];
-        {
-            if (row < p.M && col < p.N) {
-                int m = 0, local = col;
-                if constexpr (MODE == kQKV) {
-                    m = (col >= p.col_begin[1]) + (col >= p.col_begin[2]);
-                    local = col - p.col_begin[m];
-                }
-                const size_t off = static_cast<size_t>(row) * p.out_stride[m] + local;
-                _Float16 h = static_cast<_Float16>(a);
-                if (MODE == kPlain && p.residual != nullptr)
-                    h = h + __builtin_bit_cast(_Float16, p.residual[off]);  // fp16 add, RNE
-                p.out[m][off] = __builtin_bit_cast(uint16_t, h);
-            }
+        const int row = lrow + 8 * (v >> 2) + (v & 3);
+        if (cols_ok && (rows_ok || row < p.M)) {
+            const size_t off = static_cast<size_t>(row) * stride;
+            _Float16 h = static_cast<_Float16>(acc[v]);
+            if (MODE == kPlain && res != nullptr) h = h + __builtin_bit_cast(_Float16, res[off]);  // fp16 add, RNE
+            out[off] = __builtin_bit_cast(uint16_t, h);
         }
     }
 }
