@@ -26,6 +26,7 @@
 
 #include "qe_common.hpp"
 
+
 namespace qe {
 namespace {
 
@@ -265,33 +266,49 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
     auto step = [&](int kt, int d, int e, int t) __attribute__((always_inline)) {
         const int buf = kt & 1;
         if (QUAD && t == 0) load_b(min(kt / 4 + 1, KT / 4 - 1), e ^ 1);  // next quad
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            f16x8 af[MI], bf[NI];
+        auto read_a = [&](int s, f16x8 (&af)[MI]) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < MI; ++i)
                 af[i] = *reinterpret_cast<const f16x8*>(&sA[buf][(wm * WM + i * 32 + fr) * A_STRIDE + h * 32 + s * 8]);
+        };
+        auto dequant = [&](int s, f16x8 (&bf)[NI]) __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < NI; ++j) {
                 const uint32_t w = QUAD ? rb[e][j][t][s] : rb[e][j][0][s];
                 bf[j] = __builtin_bit_cast(f16x8, qwen::unpack_w4_to_half8(w, __builtin_bit_cast(_Float16, rs[e][j])));
             }
+        };
+        // software pipeline over the four sub-steps: the A fragments and the
+        // dequantized weights of sub-step s + 1 go to a second register set
+        // while the MFMAs of sub-step s run, so a wave does not stall on its
+        // own LDS latency or dequantization
+        f16x8 af[2][MI], bf[2][NI];
+        read_a(0, af[0]);
+        dequant(0, bf[0]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int c = s & 1;
+            if (s < 3) {
+                read_a(s + 1, af[c ^ 1]);
+                dequant(s + 1, bf[c ^ 1]);
+            }
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < NI; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
         }
         load_a(min(kt + D, KT - 1), d);      // step kt is consumed: refill with step kt + D
         if (!QUAD) load_b(min(kt + D, KT - 1), d);
         store_a(buf ^ 1, (d + 1) % D);        // A of step kt + 1, loaded D - 1 steps ago
-        // scheduling hint: each MFMA followed by one LDS read and three VALU
-        // ops (the dequantization), so the matrix core is fed while they issue
+        // scheduling hint: each MFMA followed by one LDS read and five VALU
+        // ops (the next sub-step's operands), so the matrix core is fed while
+        // they issue
 #pragma unroll
         for (int i = 0; i < MI * NI * 4; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
         }
         __syncthreads();
     };
