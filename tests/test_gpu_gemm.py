@@ -98,6 +98,54 @@ def test_gemm_swiglu(qe, orc, M, I, K):
     assert_fp16_close(host(out), ex, bd, ref, what="gemm swiglu")
 
 
+@pytest.mark.parametrize("K", [512, 640])  # the 256-k quad layout and the 64-k step layout
+def test_gemm_every_tile_ragged(qe, orc, K):
+    """Each block tile (64x64, 64x128, 128x64, 128x128) with one and two K
+    slices, forced, on shapes whose rows and columns end inside a tile: plain
+    with residual, QKV with head ranges off the tile grid, and SwiGLU (the
+    epilogues' partial-fragment and column-tail paths)."""
+    from helpers import ulp16
+    M, N = 37, 200
+    nq, nkv, hd = 3, 1, 40
+    I = 100
+    qw, sc = orc.synth_w4(600 + K, N, K)
+    A = _A(orc, M, K, 12)
+    R = orc.synth_f16_normal(13, M * N).reshape(M, N)
+    dims = (nq * hd, nkv * hd, nkv * hd)
+    mats = [orc.synth_w4(610 + i, n, K) for i, n in enumerate(dims)]
+    gq, gs = orc.synth_w4(620 + K, 2 * I, K)
+    ref_p, ex_p, bd_p = orc.gemm_w4a16(qw, sc, A, M, N, K, residual=R)
+    _, acc_p, _ = orc.gemm_w4a16(qw, sc, A, M, N, K)
+    refs_q = [orc.gemm_w4a16(w, s, A, M, n, K) for (w, s), n in zip(mats, dims)]
+    ref_g, ex_g, bd_g = orc.gemm_swiglu_w4a16(gq, gs, A, M, K, I)
+    dA = dev(A)
+    dw = [(dev(w), dev(s)) for w, s in mats]
+    try:
+        for tile in (1, 2, 3, 4):
+            for slices in (1, 2):
+                what = f"tile {tile} slices {slices} K {K}"
+                print(what, flush=True)
+                qe.set_tuning("gemm_tile", tile)
+                qe.set_tuning("gemm_slices", slices)
+                out = dev(R)
+                qe.launch_gemm_prefill_w4a16(dev(qw), dev(sc), dA, out, out, M, N, K)
+                assert_fp16_close(host(out), ex_p, bd_p + ulp16(acc_p) * 2.0 ** 20, ref_p, what="plain " + what)
+                outs = [empty((M, n), torch.float16) for n in dims]
+                view = qe.make_qkv_view(dw[0][0], dw[0][1], outs[0], dw[1][0], dw[1][1], outs[1], dw[2][0],
+                                        dw[2][1], outs[2])
+                qe.launch_gemm_prefill_qkv_w4a16(view, dA, M, in_features=K, num_q_heads=nq, num_kv_heads=nkv,
+                                                 head_dim=hd)
+                for o, (ref, ex, bd) in zip(outs, refs_q):
+                    assert_fp16_close(host(o), ex, bd, ref, what="qkv " + what)
+                outg = empty((M, I), torch.float16)
+                qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a16(dev(gq), dev(gs), dA, outg, M, hidden_size=K,
+                                                                 intermediate_size=I)
+                assert_fp16_close(host(outg), ex_g, bd_g, ref_g, what="swiglu " + what)
+    finally:
+        qe.set_tuning("gemm_tile", 0)
+        qe.set_tuning("gemm_slices", 0)
+
+
 def _torch_ref(orc, qw, sc, A, N, K):
     wdq = torch.from_numpy(orc.dequant_w4_f16(qw, sc, N, K)).cuda().float()
     a = torch.from_numpy(A).cuda().float()
