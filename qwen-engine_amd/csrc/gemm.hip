@@ -348,6 +348,205 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
             for (int v = 0; v < 16; ++v) mine[((i * NI + j) * 16 + v) * 256 + tid] = acc[i][j][v];
 }
 
+// K % 256 == 0, 512 threads: two groups of four waves split the k steps of
+// the tile between them (group g takes the steps 2 i + g, i.e. steps g and
+// g + 2 of every 256-k quad), each with its own A staging, and add their
+// accumulators through LDS at the end.  For grids of at most one block per
+// CU (M = 128 prefill) this gives every SIMD two waves without split-K
+// partials in memory.  Per group the step is the register-staged kernel's:
+// A through a 4-stage register ring and a double-buffered LDS tile, weights
+// a quad ahead (the group's two 16-byte pieces of each column and quad),
+// the four sub-steps software-pipelined.
+template <int BM, int BN, int WGM, int MODE>
+__global__ __launch_bounds__(512, 1) void gemm_w4a16_ks2_kernel(GemmParams p) {
+    constexpr int WGN = 4 / WGM;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int MI = WM / 32, NI = WN / 32;
+    constexpr int A_U4 = BM / 32;
+    constexpr int D = 4;
+    constexpr int TILE_H = BM * A_STRIDE;
+    static_assert(MI >= 1 && NI >= 1, "wave tile");
+    __shared__ __align__(16) _Float16 sA[2][2][TILE_H];  // [group][buffer]
+    static_assert(sizeof(sA) >= sizeof(float) * MI * NI * 16 * 256, "the group exchange reuses the A tiles");
+
+    const int tid = threadIdx.x;
+    const int kg = tid >> 8;      // k group
+    const int gtid = tid & 255;   // thread within the group
+    const int lane = tid & 63;
+    const int wave = gtid >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int m0 = blockIdx.y * BM;
+    const int n0 = blockIdx.x * BN;
+    const int K = p.K;
+    const int G = K >> 7;
+    const int slices = gridDim.z;
+    const int U_all = K / (BK * 4);
+    const int kt_begin = 4 * static_cast<int>((static_cast<long long>(blockIdx.z) * U_all) / slices);
+    const int kt_end = 4 * static_cast<int>((static_cast<long long>(blockIdx.z + 1) * U_all) / slices);
+    const int KTL = (kt_end - kt_begin) / 2;  // steps per group
+    const int fr = lane & 31;
+    const int h = lane >> 5;
+
+    const int a_row = gtid >> 3;
+    const int c = gtid & 7;
+    const int a_col = c * 8;
+    const int a_k = 128 * (c >> 2) + 8 * (c & 3);
+    const uint16_t* a_src[A_U4];
+#pragma unroll
+    for (int i = 0; i < A_U4; ++i)
+        a_src[i] = p.A + static_cast<size_t>(min(m0 + a_row + 32 * i, p.M - 1)) * K + a_k;
+    // local step i of group kg is global step 2 i + kg of the slice
+    auto a_koff = [&](int i) __attribute__((always_inline)) {
+        const int g = kt_begin + 2 * i + kg;
+        return 256 * (g >> 2) + 32 * (g & 3);
+    };
+    const u32x4* b_src[NI];
+    const uint16_t* b_sc[NI];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        const int col = min(n0 + wn * WN + j * 32 + fr, p.N - 1);
+        int m = 0, local = col;
+        if constexpr (MODE == kQKV) {
+            m = (col >= p.col_begin[1]) + (col >= p.col_begin[2]);
+            local = col - p.col_begin[m];
+        }
+        b_src[j] = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(local) * (K >> 3)) + 4 * h + kg;
+        b_sc[j] = p.sc[m] + static_cast<size_t>(local) * G + h;
+    }
+
+    u32x4 ra[D][A_U4];
+    u32x4 rb[2][NI][2];  // [quad buffer][column][the group's two steps of the quad]
+    uint16_t rs[2][NI];
+    auto load_a = [&](int i, int d) __attribute__((always_inline)) {
+        const int k0 = a_koff(i);
+#pragma unroll
+        for (int u = 0; u < A_U4; ++u) ra[d][u] = *reinterpret_cast<const u32x4*>(a_src[u] + k0);
+    };
+    auto load_b = [&](int qd, int e) __attribute__((always_inline)) {
+        const int g = (kt_begin >> 2) + qd;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            rb[e][j][0] = b_src[j][8 * g];
+            rb[e][j][1] = b_src[j][8 * g + 2];
+            rs[e][j] = b_sc[j][2 * g];
+        }
+    };
+    auto store_a = [&](int buf, int d) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < A_U4; ++u)
+            *reinterpret_cast<u32x4*>(&sA[kg][buf][(a_row + 32 * u) * A_STRIDE + a_col]) = ra[d][u];
+    };
+    auto read_a = [&](int buf, int s, f16x8 (&af)[MI]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+            af[i] = *reinterpret_cast<const f16x8*>(&sA[kg][buf][(wm * WM + i * 32 + fr) * A_STRIDE + h * 32 + s * 8]);
+    };
+    auto dequant = [&](int e, int tt, int s, f16x8 (&bf)[NI]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+            bf[j] = __builtin_bit_cast(f16x8, qwen::unpack_w4_to_half8(rb[e][j][tt][s],
+                                                                        __builtin_bit_cast(_Float16, rs[e][j])));
+    };
+
+    f32x16 acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = f32x16{};
+
+    load_b(0, 0);
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_a(min(d, KTL - 1), d);
+    store_a(0, 0);
+    __syncthreads();
+
+    // local step i: ring slot d = i % D, LDS buffer i % 2, quad i / 2 in
+    // buffer e = (i / 2) % 2, the group's piece tt = i % 2 of it
+    auto step = [&](int i, int d, int e, int tt) __attribute__((always_inline)) {
+        const int buf = i & 1;
+        if (tt == 0) load_b(min(i / 2 + 1, KTL / 2 - 1), e ^ 1);  // next quad
+        f16x8 af[2][MI], bf[2][NI];
+        read_a(buf, 0, af[0]);
+        dequant(e, tt, 0, bf[0]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int cs = s & 1;
+            if (s < 3) {
+                read_a(buf, s + 1, af[cs ^ 1]);
+                dequant(e, tt, s + 1, bf[cs ^ 1]);
+            }
+#pragma unroll
+            for (int a = 0; a < MI; ++a)
+#pragma unroll
+                for (int j = 0; j < NI; ++j)
+                    acc[a][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cs][a], bf[cs][j], acc[a][j], 0, 0, 0);
+        }
+        load_a(min(i + D, KTL - 1), d);
+        store_a(buf ^ 1, (d + 1) % D);
+#pragma unroll
+        for (int x = 0; x < MI * NI * 4; ++x) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        }
+        __syncthreads();
+    };
+    int i = 0;
+    for (; i + 4 <= KTL; i += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) step(i + u, u % D, (u / 2) & 1, u & 1);
+    }
+    if (i < KTL) {  // KTL is even: two steps (one quad) left
+#pragma unroll
+        for (int u = 0; u < 2; ++u) step(i + u, u % D, 0, u);
+    }
+
+    // the groups add their accumulators: group 0 keeps fragments a < MI / 2
+    // (all when MI == 1: then group 1 hands over everything), group 1 the rest;
+    // each writes the fragments the other keeps into the (now idle) A tiles
+    constexpr int KEEP0 = MI == 1 ? 1 : MI / 2;
+    float* xch = reinterpret_cast<float*>(&sA[0][0][0]);
+    auto slot = [&](int a, int j, int v) __attribute__((always_inline)) {
+        return ((a * NI + j) * 16 + v) * 256 + gtid;
+    };
+#pragma unroll
+    for (int a = 0; a < MI; ++a) {
+        const bool mine = kg == 0 ? a < KEEP0 : a >= KEEP0;
+        if (!mine)
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) xch[slot(a, j, v)] = acc[a][j][v];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int a = 0; a < MI; ++a) {
+        const bool mine = kg == 0 ? a < KEEP0 : a >= KEEP0;
+        if (mine)
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[a][j][v] += xch[slot(a, j, v)];
+    }
+    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const int n_tiles = gridDim.x * gridDim.y;
+    float* part = g_splitk_ws + (static_cast<size_t>(blockIdx.z) * n_tiles + tile) * (BM * BN);
+#pragma unroll
+    for (int a = 0; a < MI; ++a) {
+        const bool mine = kg == 0 ? a < KEEP0 : a >= KEEP0;
+        if (!mine) continue;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            if (slices == 1) {
+                epilogue_frag<MODE>(p, acc[a][j], m0 + wm * WM + a * 32, n0 + wn * WN + j * 32 + fr, lane);
+            } else {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) part[((a * NI + j) * 16 + v) * 256 + gtid] = acc[a][j][v];
+            }
+        }
+    }
+}
+
 // Sums the K-slice partials in slice order and applies the epilogue.  grid
 // (N tiles, M tiles, fragments): block z takes the 32x32 fragment z of its
 // tile, 256 threads in the MFMA lane layout of the 4 waves.  S > 0: all S
@@ -401,6 +600,16 @@ void launch_reduce(const GemmParams& p, dim3 tiles, int slices, hipStream_t s) {
 template <int BM, int BN, int WGM, int MODE>
 void launch_tiles(const GemmParams& p, int slices, hipStream_t s) {
     const dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, slices);
+    // two k groups per block when the grid leaves every CU with at most one
+    // block (its SIMDs would otherwise run one wave each)
+    const int ks2 = gemm_ks2_mode();
+    const bool two = p.K % 256 == 0 && ks2 != 1 &&
+                     (ks2 == 2 || static_cast<long long>(grid.x) * grid.y * grid.z <= cu_count());
+    if (two) {
+        gemm_w4a16_ks2_kernel<BM, BN, WGM, MODE><<<grid, 512, 0, s>>>(p);
+        if (slices > 1) launch_reduce<BM, BN, WGM, MODE>(p, grid, slices, s);
+        return;
+    }
     if (p.K % 256 == 0)
         gemm_w4a16_mfma_kernel<BM, BN, WGM, MODE, true><<<grid, 256, 0, s>>>(p);
     else

@@ -26,6 +26,7 @@ int cu_count();
 int gemm_split_k_enabled();
 int gemm_forced_tile();    // 0 auto, 1 64x64, 2 64x128 (1x4 waves), 3 128x64, 4 128x128 (1x4 waves)
 int gemm_forced_slices();  // 0 auto, else K slices
+int gemm_ks2_mode();       // 0 auto, 1 never, 2 always (K % 256 == 0): the two-group k split
 int gemv_forced_bt();      // 0 auto, else GEMV block size (256, 512, 1024)
 int gemv_forced_cap();     // 0 auto, else the largest GEMV grid (larger grids loop over row sets)
 

@@ -17,6 +17,7 @@ int g_cu_count[64] = {0};
 int g_gemm_split_k = 1;
 int g_gemm_tile = 0;
 int g_gemm_slices = 0;
+int g_gemm_ks2 = 0;
 int g_gemv_bt = 0;
 int g_gemv_cap = 0;
 }  // namespace
@@ -24,6 +25,7 @@ int g_gemv_cap = 0;
 int gemm_split_k_enabled() { return g_gemm_split_k; }
 int gemm_forced_tile() { return g_gemm_tile; }
 int gemm_forced_slices() { return g_gemm_slices; }
+int gemm_ks2_mode() { return g_gemm_ks2; }
 int gemv_forced_bt() { return g_gemv_bt; }
 int gemv_forced_cap() { return g_gemv_cap; }
 
@@ -74,6 +76,11 @@ extern "C" int qe_set_tuning(const char* key, int value) {
         if (value < 0 || value > 65536)
             return qe::fail(QE_ERR_INVALID_ARGUMENT, "set_tuning: gemv_grid_cap %d not in 0..65536", value);
         qe::g_gemv_cap = value;
+        return QE_OK;
+    }
+    if (std::strcmp(key, "gemm_ks2") == 0) {
+        if (value < 0 || value > 2) return qe::fail(QE_ERR_INVALID_ARGUMENT, "set_tuning: gemm_ks2 %d not in 0..2", value);
+        qe::g_gemm_ks2 = value;
         return QE_OK;
     }
     if (std::strcmp(key, "gemm_slices") == 0) {
