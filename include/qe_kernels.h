@@ -312,6 +312,9 @@ int qe_stream_read(const void* data, size_t bytes, uint32_t* sink, hipStream_t s
  *   block tile: 1 64x64, 2 64x128, 3 128x64, 4 128x128 (rows x columns);
  *   "gemm_slices" 0..64 (default 0 = chosen per shape) - force the number of
  *   K slices;
+ *   "gemm_ks2" 0..2 (default 0) - prefill GEMMs with K % 256 == 0 split the k
+ *   steps of a block over two groups of four waves: 0 when the grid has at
+ *   most one block per CU, 1 never, 2 always;
  *   "gemv_block" 0, 256, 512, 1024 (default 0 = chosen per shape) - force the
  *   decode GEMV block size;
  *   "gemv_grid_cap" 0..65536 (default 0 = 8 blocks of 256 threads per CU) -
