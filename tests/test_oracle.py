@@ -247,16 +247,87 @@ def test_gemm_against_numpy(orc):
 
 
 # ------------------------------------------------------- norm / argmax -----
-def test_rmsnorm(orc):
-    rng = np.random.default_rng(10)
+def _f16(v):
+    """Round a float64 value once to fp16 (round to nearest even)."""
+    return float(np.float16(v))
+
+
+def _rms_closed(x_i, mean_sq, gamma_i, eps=1e-6, divisor_fix=1.0, eps_outside=False,
+                round_inv=True, one_rounding=False):
+    """Closed form of one RMSNorm output for inputs whose mean square is known
+    exactly (constant vectors, one-hot vectors), in float64 with one fp16
+    rounding per fp16 operation of rmsnorm_rope.cu:214-227.  The keyword
+    arguments produce the plausible misreadings the tests must reject."""
+    m = mean_sq * divisor_fix
+    inv = 1.0 / (np.sqrt(m) + eps) if eps_outside else 1.0 / np.sqrt(m + eps)
+    h = _f16(inv) if round_inv else inv
+    if one_rounding:
+        return _f16(x_i * h * gamma_i)
+    return _f16(_f16(x_i * h) * gamma_i)
+
+
+def test_rmsnorm_constant_vector_closed_form(orc):
+    """x = c (every element), gamma = g: mean(x^2) = c^2 exactly, so every
+    output is fp16(fp16(c * fp16(1/sqrt(c^2 + eps))) * g)."""
     H = 1536
-    x = rng.standard_normal((3, H)).astype(np.float16)
-    g = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
-    got = orc.rmsnorm_fp16(x, g)
-    xf = x.astype(np.float32)
-    inv = (np.float32(1) / np.sqrt((xf.astype(np.float64) ** 2).sum(1).astype(np.float32) / np.float32(H) + np.float32(1e-6))).astype(np.float16)
-    ref = ((xf * inv[:, None].astype(np.float32)).astype(np.float16).astype(np.float32) * g.astype(np.float32)).astype(np.float16)
-    assert np.array_equal(got, ref)
+    cs = [3.0, -3.0, 0.5, 1.25, 0.0078125, 0.00390625, 7.0, 100.0, 0.2998046875,
+          1.099609375, 0.7001953125, -2.19921875, 1.7001953125]
+    gs = [1.0, 1.5, 0.7998046875, 3.0]
+    caught = {"eps_outside": 0, "no_eps": 0, "unrounded_inv": 0, "one_rounding": 0}
+    for c in cs:
+        for g in gs:
+            x = np.full((1, H), c, np.float16)
+            gamma = np.full(H, g, np.float16)
+            got = orc.rmsnorm_fp16(x, gamma).astype(np.float64)
+            want = _rms_closed(c, c * c, g)
+            assert np.all(got == want), (c, g, got[0, 0], want)
+            caught["eps_outside"] += want != _rms_closed(c, c * c, g, eps_outside=True)
+            caught["no_eps"] += want != _rms_closed(c, c * c, g, eps=0.0)
+            caught["unrounded_inv"] += want != _rms_closed(c, c * c, g, round_inv=False)
+            caught["one_rounding"] += want != _rms_closed(c, c * c, g, one_rounding=True)
+    # the chosen inputs tell every misreading apart from the reference formula
+    assert all(v > 0 for v in caught.values()), caught
+
+
+def test_rmsnorm_one_hot_closed_form(orc):
+    """x = a * e_i: mean(x^2) = a^2 / H, element i becomes
+    fp16(fp16(a * fp16(1/sqrt(a^2/H + eps))) * gamma_i) ~ sign(a) sqrt(H) and
+    every other element is exactly zero."""
+    caught_divisor = 0
+    for H in (128, 256, 1536, 8960):
+        for a, i in ((1.0, 0), (-2.5, 7), (0.125, 127), (60000.0, 5), (0.0009765625, 3)):
+            x = np.zeros((1, H), np.float16)
+            x[0, i] = a
+            gamma = np.full(H, 1.0, np.float16)
+            gamma[i] = 0.5
+            got = orc.rmsnorm_fp16(x, gamma)[0].astype(np.float64)
+            want = _rms_closed(a, a * a / H, 0.5)
+            assert got[i] == want, (H, a, got[i], want)
+            assert np.count_nonzero(np.delete(got, i)) == 0
+            if abs(a) >= 1.0:  # eps is negligible
+                assert abs(abs(got[i]) - 0.5 * np.sqrt(H)) <= 0.01 * np.sqrt(H)
+            caught_divisor += want != _rms_closed(a, a * a / H, 0.5, divisor_fix=H / (H - 1))
+    assert caught_divisor > 0  # a divisor of H - 1 fails this test
+
+
+def test_rmsnorm_symmetries(orc):
+    """rmsnorm(-x) = -rmsnorm(x) bit for bit; doubling gamma doubles every
+    output exactly (fp16 multiplication by 2 is exact away from overflow)."""
+    rng = np.random.default_rng(10)
+    for H in (128, 1536, 8960):
+        x = rng.standard_normal((3, H)).astype(np.float16)
+        g = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
+        y = orc.rmsnorm_fp16(x, g)
+        assert np.array_equal(orc.rmsnorm_fp16(-x, g).view(np.uint16), (-y).view(np.uint16))
+        y2 = orc.rmsnorm_fp16(x, (g.astype(np.float32) * 2).astype(np.float16))
+        normal = np.abs(y.astype(np.float32)) >= 2.0 ** -14  # subnormals round on a fixed grid
+        assert normal.mean() > 0.99
+        assert np.array_equal(y2[normal], (y.astype(np.float32) * 2).astype(np.float16)[normal])
+        # rows are independent
+        assert np.array_equal(orc.rmsnorm_fp16(x[1:2], g), y[1:2])
+        # the output's RMS is |gamma|-weighted 1 within fp16 rounding
+        rms = np.sqrt(np.mean((y.astype(np.float64) / g.astype(np.float64)) ** 2, axis=1))
+        assert np.all(np.abs(rms - 1) < 2e-3)
 
 
 def test_argmax_tie_break_and_nan(orc):
