@@ -101,7 +101,8 @@ def main():
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        # capture on the warm-up stream: it already holds the split-K workspace
+        with torch.cuda.graph(g, stream=s):
             for i in range(reps):
                 fn(i)
         return g

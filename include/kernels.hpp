@@ -5,8 +5,10 @@
 // qe_kernels.h and throws std::runtime_error on failure, as the reference's
 // CUDA_KERNEL_CHECK does (include/tensor.cuh:11-23).
 //
-// Only the launchers of the matrix path are declared here (plus greedy
-// sample_and_advance); embedding, RoPE and attention are outside this library.
+// Every launcher of kernels.cuh that src/engine.cu calls is declared here:
+// the matrix path, and the embedding, RoPE/KV-append, attention and sampling
+// launchers of the decode and prefill loops.  The prefill GEMMs that split K
+// keep their partial sums in a workspace per stream (see qe_kernels.h).
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -63,6 +65,16 @@ inline void launch_rmsnorm_q8_1(const half* input, const half* gamma, half* outp
     detail::check(qe_launch_rmsnorm_q8_1(detail::h(input), detail::h(gamma), detail::h(output_fp16_opt), out_q8,
                                          out_scale, out_sum8, stream, hidden_size),
                   "launch_rmsnorm_q8_1");
+}
+
+// include/kernels.cuh:11-20
+inline void launch_embed_lookup_w4a16(const uint32_t* embed_qweight, const half* embed_scales,
+                                      const int32_t* d_token_ids, half* out_hidden,
+                                      const DeviceControlBlock* d_control, int num_tokens, hipStream_t stream,
+                                      int hidden_size = HIDDEN_SIZE) {
+    detail::check(qe_launch_embed_lookup_w4a16(embed_qweight, detail::h(embed_scales), d_token_ids,
+                                               detail::h(out_hidden), d_control, num_tokens, stream, hidden_size),
+                  "launch_embed_lookup_w4a16");
 }
 
 // include/kernels.cuh:30-37
@@ -158,6 +170,49 @@ inline void launch_gemm_prefill_dual_gate_up_swiglu_w4a16(const uint32_t* gate_u
                                                                    detail::h(input_x), detail::h(output_mlp), M,
                                                                    stream, hidden_size, intermediate_size),
                   "launch_gemm_prefill_dual_gate_up_swiglu_w4a16");
+}
+
+// include/kernels.cuh:156-174
+inline void launch_qkv_bias_rope_kv_append(half* q, half* k, half* v, const half* q_bias, const half* k_bias,
+                                           const half* v_bias, half* layer_k_cache, half* layer_v_cache,
+                                           const DeviceControlBlock* d_control, int num_tokens, hipStream_t stream,
+                                           int num_q_heads = NUM_Q_HEADS, int num_kv_heads = NUM_KV_HEADS,
+                                           int head_dim = HEAD_DIM, int max_seq_len = MAX_SEQ_LEN,
+                                           int rotary_dim = 0, float rope_theta = ROPE_THETA) {
+    detail::check(qe_launch_qkv_bias_rope_kv_append(detail::h(q), detail::h(k), detail::h(v), detail::h(q_bias),
+                                                    detail::h(k_bias), detail::h(v_bias), detail::h(layer_k_cache),
+                                                    detail::h(layer_v_cache), d_control, num_tokens, stream,
+                                                    num_q_heads, num_kv_heads, head_dim, max_seq_len, rotary_dim,
+                                                    rope_theta),
+                  "launch_qkv_bias_rope_kv_append");
+}
+
+// include/kernels.cuh:177-193
+inline void launch_attention_gqa_flash_decode(const half* q, const half* layer_k_cache, const half* layer_v_cache,
+                                              float* splitk_partial_out, float* splitk_partial_lse, half* attn_out,
+                                              const DeviceControlBlock* d_control, hipStream_t stream,
+                                              int num_q_heads = NUM_Q_HEADS, int num_kv_heads = NUM_KV_HEADS,
+                                              int head_dim = HEAD_DIM, int max_seq_len = MAX_SEQ_LEN,
+                                              int8_t* out_q8 = nullptr, float* out_scale = nullptr,
+                                              int32_t* out_sum8 = nullptr) {
+    detail::check(qe_launch_attention_gqa_flash_decode(detail::h(q), detail::h(layer_k_cache),
+                                                       detail::h(layer_v_cache), splitk_partial_out,
+                                                       splitk_partial_lse, detail::h(attn_out), d_control, stream,
+                                                       num_q_heads, num_kv_heads, head_dim, max_seq_len, out_q8,
+                                                       out_scale, out_sum8),
+                  "launch_attention_gqa_flash_decode");
+}
+
+// include/kernels.cuh:195-207
+inline void launch_attention_gqa_prefill(const half* q, const half* layer_k_cache, const half* layer_v_cache,
+                                         half* attn_out, const DeviceControlBlock* d_control, int num_tokens,
+                                         hipStream_t stream, int num_q_heads = NUM_Q_HEADS,
+                                         int num_kv_heads = NUM_KV_HEADS, int head_dim = HEAD_DIM,
+                                         int max_seq_len = MAX_SEQ_LEN, int hidden_size = HIDDEN_SIZE) {
+    detail::check(qe_launch_attention_gqa_prefill(detail::h(q), detail::h(layer_k_cache), detail::h(layer_v_cache),
+                                                  detail::h(attn_out), d_control, num_tokens, stream, num_q_heads,
+                                                  num_kv_heads, head_dim, max_seq_len, hidden_size),
+                  "launch_attention_gqa_prefill");
 }
 
 // include/kernels.cuh:209-217 (greedy decoding)

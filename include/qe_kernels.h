@@ -10,9 +10,16 @@
  *   - Q8_1 activations are int8 q8[K], fp32 scale[K/128], int32 sum8[K/8]
  *     with sum8 = -8 * (sum of the 8 q8 values it covers),
  *   - `stream` is a hipStream_t (NULL = the null stream).
- * Every call is asynchronous on `stream`, allocates nothing, never
- * synchronizes, and is safe under HIP graph capture.  `residual` may alias
- * the output.  A NULL optional pointer means "skip", as in the reference.
+ * Every call is asynchronous on `stream`, never synchronizes, and is safe
+ * under HIP graph capture.  `residual` may alias the output.  A NULL
+ * optional pointer means "skip", as in the reference.  No call allocates,
+ * except that the prefill GEMMs, when they split K over several blocks,
+ * keep fp32 partial sums in a 32 MiB workspace that belongs to the stream:
+ * the first such launch on a stream allocates it (hipMalloc, outside graph
+ * capture only) and it is kept until the process ends.  GEMMs on different
+ * streams therefore never share partials.  A launch being captured on a
+ * stream that has no workspace yet runs without K slices (same results,
+ * different speed); qe_gemm_reserve_workspace() allocates one ahead.
  *
  * Return value: QE_OK, or a QE_ERR_* code; qe_last_error() then describes
  * the failure (thread-local).  The C++ mirror in kernels.hpp turns a
@@ -130,10 +137,20 @@ int qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(const uint16_t* input, cons
 
 /* ---- prefill dequant-GEMM (MFMA) ----------------------------------------- */
 
+/* Allocates the split-K workspace of `stream` on the current device now (it
+ * is otherwise allocated by the first prefill GEMM on the stream that runs
+ * outside graph capture).  Call it before capturing prefill GEMMs into a
+ * graph on a new stream.  At most 64 streams per device hold one; later
+ * streams run their GEMMs without K slices.  No counterpart in the
+ * reference (its GEMMs never split K). */
+int qe_gemm_reserve_workspace(hipStream_t stream);
+
 /* Replaces launch_gemm_prefill_w4a16, include/kernels.cuh:119-130.
  * Y[M,N] = fp16(A[M,K] . dequant(W)[N,K]^T), fp32 accumulation;
  * residual added as fp16(fp16(acc) + residual).  `sm_count` is accepted for
- * signature parity; tile selection uses the device's CU count. */
+ * signature parity; tile selection uses the device's CU count.  K-slice
+ * partials are summed in slice order, so a given plan is deterministic; a
+ * launch without a workspace (see above) may round differently in fp32. */
 int qe_launch_gemm_prefill_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* input_x,
                                  const uint16_t* residual, uint16_t* output_y, int M, int N, int K,
                                  hipStream_t stream, int sm_count);

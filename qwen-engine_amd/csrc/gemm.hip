@@ -23,6 +23,7 @@
 //     (blocks per CU, steps per block, split-K overhead); split-K partials
 //     are reduced by a second kernel in slice order.
 #include <algorithm>
+#include <mutex>
 
 #include "qe_common.hpp"
 
@@ -51,6 +52,7 @@ struct GemmParams {
     const int8_t* A8;         // W4A8 variant: Q8_1 rows of the activation
     const float* A8_scale;
     const int32_t* A8_sum8;
+    float* ws;         // split-K partials (slices > 1 only)
     int M, N, K;       // N = virtual columns (SwiGLU: 2*I)
 };
 
@@ -60,14 +62,12 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return g * u * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.44269504088896341f * g));
 }
 
-// Split-K scratch: fp32 partial tiles of the K slices, reduced by a second
-// kernel on the same stream (deterministic order, no atomics or fences).  A
-// file-scope device array, so launches stay allocation-free and
-// graph-capture safe.  Split-K launches issued concurrently on different
-// streams of one device would share it; the engine issues its GEMMs on one
-// stream.
+// Split-K partials: fp32 tiles of the K slices, reduced by a second kernel
+// on the same stream (deterministic order, no atomics or fences).  They live
+// in a workspace of kWsFloats floats that belongs to the launching stream
+// (gemm_workspace below), so GEMMs in flight on different streams never
+// share partials.
 constexpr size_t kWsFloats = size_t(8) << 20;  // 32 MiB
-__device__ float g_splitk_ws[kWsFloats];
 
 // One 32x32 accumulator fragment whose rows start at r0 and whose lane
 // column is col.  D[i][j] of a 32x32 MFMA tile: j = lane%32,
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
     }
     const int tile = blockIdx.y * gridDim.x + blockIdx.x;
     const int n_tiles = gridDim.x * gridDim.y;
-    float* mine = g_splitk_ws + (static_cast<size_t>(blockIdx.z) * n_tiles + tile) * (BM * BN);
+    float* mine = p.ws + (static_cast<size_t>(blockIdx.z) * n_tiles + tile) * (BM * BN);
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -530,7 +530,7 @@ __global__ __launch_bounds__(512, 1) void gemm_w4a16_ks2_kernel(GemmParams p) {
     }
     const int tile = blockIdx.y * gridDim.x + blockIdx.x;
     const int n_tiles = gridDim.x * gridDim.y;
-    float* part = g_splitk_ws + (static_cast<size_t>(blockIdx.z) * n_tiles + tile) * (BM * BN);
+    float* part = p.ws + (static_cast<size_t>(blockIdx.z) * n_tiles + tile) * (BM * BN);
 #pragma unroll
     for (int a = 0; a < MI; ++a) {
         const bool mine = kg == 0 ? a < KEEP0 : a >= KEEP0;
@@ -561,7 +561,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmParams p, i
     const int n_tiles = gridDim.x * gridDim.y;
     const int f = blockIdx.z, i = f / NI, j = f % NI;
     const size_t slice_stride = static_cast<size_t>(n_tiles) * (BM * BN);
-    const float* part = g_splitk_ws + static_cast<size_t>(tile) * (BM * BN) + f * 16 * 256 + tid;
+    const float* part = p.ws + static_cast<size_t>(tile) * (BM * BN) + f * 16 * 256 + tid;
     f32x16 acc = f32x16{};
     if constexpr (S > 0) {
         float x[S][16];
@@ -646,14 +646,16 @@ float predict_us(const TileCost& t, int M, int N, int K, int slices, int cus) {
 }
 
 template <int MODE>
-int launch_gemm(const GemmParams& p, hipStream_t stream, const char* what) {
+int launch_gemm(GemmParams p, hipStream_t stream, const char* what, float* ws, size_t ws_floats) {
     if (p.M <= 0 || p.N <= 0) return QE_OK;
+    p.ws = ws;
+    if (ws == nullptr) ws_floats = 0;
     const int cus = cu_count();
     const int KT = p.K / BK;
     const int max_slices = (p.K % 256 == 0) ? KT / 4 : KT;  // QUAD slices whole 256-k quads
     auto fits = [&](const TileCost& t, int s) {
         const size_t tiles = static_cast<size_t>((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn);
-        return s == 1 || (s <= max_slices && KT / s >= 4 && static_cast<size_t>(s) * tiles * t.bm * t.bn <= kWsFloats);
+        return s == 1 || (s <= max_slices && KT / s >= 4 && static_cast<size_t>(s) * tiles * t.bm * t.bn <= ws_floats);
     };
     int ti = 0, slices = 1;
     float best = 1e30f;
@@ -824,7 +826,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a8_mfma_kernel(GemmParams p) {
     }
     const int tile = blockIdx.y * gridDim.x + blockIdx.x;
     const int n_tiles = gridDim.x * gridDim.y;
-    float* mine = g_splitk_ws + (static_cast<size_t>(blockIdx.z) * n_tiles + tile) * (BM * BN);
+    float* mine = p.ws + (static_cast<size_t>(blockIdx.z) * n_tiles + tile) * (BM * BN);
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -832,8 +834,10 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a8_mfma_kernel(GemmParams p) {
 }
 
 template <int MODE>
-int launch_gemm_w4a8(const GemmParams& p, hipStream_t stream, const char* what) {
+int launch_gemm_w4a8(GemmParams p, hipStream_t stream, const char* what, float* ws, size_t ws_floats) {
     if (p.M <= 0 || p.N <= 0) return QE_OK;
+    p.ws = ws;
+    if (ws == nullptr) ws_floats = 0;
     // 128-row tiles when they already give one block per CU, else 64-row tiles
     const int cus = cu_count();
     const int nt128 = ((p.M + 127) / 128) * ((p.N + 127) / 128);
@@ -846,7 +850,7 @@ int launch_gemm_w4a8(const GemmParams& p, hipStream_t stream, const char* what) 
     int slices = 1;  // about two blocks per CU, >= 4 groups per slice
     if (tiles < cus && gemm_split_k_enabled()) slices = std::max(1, std::min((2 * cus + tiles - 1) / tiles, G / 4));
     if (const int f = gemm_forced_slices()) slices = std::max(1, std::min(f, G));
-    while (slices > 1 && static_cast<size_t>(slices) * tiles * bm * 128 > kWsFloats) --slices;
+    while (slices > 1 && static_cast<size_t>(slices) * tiles * bm * 128 > ws_floats) --slices;
     const dim3 g3(grid.x, grid.y, slices);
     if (big) gemm_w4a8_mfma_kernel<128, MODE><<<g3, 256, 0, stream>>>(p);
     else gemm_w4a8_mfma_kernel<64, MODE><<<g3, 256, 0, stream>>>(p);
@@ -856,6 +860,56 @@ int launch_gemm_w4a8(const GemmParams& p, hipStream_t stream, const char* what) 
     }
     return check_launch(what);
 }
+
+// The split-K workspace of `stream` on the current device: allocated by the
+// first launch on that stream that is not being captured into a graph, then
+// kept until the process ends (at most kMaxWsStreams per device; further
+// streams and captures on a stream without one run without K slices).
+constexpr int kMaxWsStreams = 64;
+struct WsSlot {
+    hipStream_t stream;
+    float* ptr;
+};
+std::mutex g_ws_mutex;
+WsSlot g_ws[64][kMaxWsStreams];
+int g_ws_count[64];
+
+float* gemm_workspace(hipStream_t stream) {
+    if (!gemm_split_k_enabled()) return nullptr;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    for (int i = 0; i < g_ws_count[dev]; ++i)
+        if (g_ws[dev][i].stream == stream) return g_ws[dev][i].ptr;
+    if (g_ws_count[dev] == kMaxWsStreams) return nullptr;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &st) != hipSuccess || st != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    void* ptr = nullptr;
+    if (hipMalloc(&ptr, kWsFloats * sizeof(float)) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    g_ws[dev][g_ws_count[dev]++] = WsSlot{stream, static_cast<float*>(ptr)};
+    return static_cast<float*>(ptr);
+}
+
+}  // namespace
+}  // namespace qe
+
+extern "C" int qe_gemm_reserve_workspace(hipStream_t stream) {
+    if (!qe::gemm_split_k_enabled()) return QE_OK;
+    if (qe::gemm_workspace(stream) == nullptr)
+        return qe::fail(QE_ERR_HIP, "gemm_reserve_workspace: no workspace (stream capturing, allocation failed or "
+                                    "%d streams already hold one)", qe::kMaxWsStreams);
+    qe::clear_error();
+    return QE_OK;
+}
+
+namespace qe {
+namespace {
 
 int check_gemm_common(const char* what, const uint16_t* A, int M, int K) {
     QE_REQUIRE(A != nullptr, "%s: input_x is NULL", what);
@@ -889,7 +943,7 @@ extern "C" int qe_launch_gemm_prefill_w4a16(const uint32_t* qweight, const uint1
     p.M = M;
     p.N = N;
     p.K = K;
-    return launch_gemm<kPlain>(p, stream, what);
+    return launch_gemm<kPlain>(p, stream, what, gemm_workspace(stream), kWsFloats);
 }
 
 extern "C" int qe_launch_gemm_prefill_qkv_w4a16(const qe_qkv_view* view, const uint16_t* input_x, int M,
@@ -923,7 +977,7 @@ extern "C" int qe_launch_gemm_prefill_qkv_w4a16(const qe_qkv_view* view, const u
     p.M = M;
     p.N = q_dim + 2 * kv_dim;
     p.K = in_features;
-    return launch_gemm<kQKV>(p, stream, what);
+    return launch_gemm<kQKV>(p, stream, what, gemm_workspace(stream), kWsFloats);
 }
 
 extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_qweight,
@@ -946,7 +1000,7 @@ extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(const uint32_t* 
     p.M = M;
     p.N = 2 * intermediate_size;
     p.K = hidden_size;
-    return launch_gemm<kSwiglu>(p, stream, what);
+    return launch_gemm<kSwiglu>(p, stream, what, gemm_workspace(stream), kWsFloats);
 }
 
 // ---- W4A8 prefill GEMM entry points --------------------------------------------------
@@ -980,7 +1034,7 @@ extern "C" int qe_launch_gemm_prefill_w4a8(const uint32_t* qweight, const uint16
     p.M = M;
     p.N = N;
     p.K = K;
-    return launch_gemm_w4a8<kPlain>(p, stream, what);
+    return launch_gemm_w4a8<kPlain>(p, stream, what, gemm_workspace(stream), kWsFloats);
 }
 
 extern "C" int qe_launch_gemm_prefill_qkv_w4a8(const qe_qkv_view* view, const int8_t* input_q8,
@@ -1016,7 +1070,7 @@ extern "C" int qe_launch_gemm_prefill_qkv_w4a8(const qe_qkv_view* view, const in
     p.M = M;
     p.N = q_dim + 2 * kv_dim;
     p.K = in_features;
-    return launch_gemm_w4a8<kQKV>(p, stream, what);
+    return launch_gemm_w4a8<kQKV>(p, stream, what, gemm_workspace(stream), kWsFloats);
 }
 
 extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a8(const uint32_t* gate_up_qweight,
@@ -1041,5 +1095,5 @@ extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a8(const uint32_t* g
     p.M = M;
     p.N = 2 * intermediate_size;
     p.K = hidden_size;
-    return launch_gemm_w4a8<kSwiglu>(p, stream, what);
+    return launch_gemm_w4a8<kSwiglu>(p, stream, what, gemm_workspace(stream), kWsFloats);
 }

@@ -57,6 +57,7 @@ SIGNATURES = {
 OTHER_SIGNATURES = {
     "qe_stream_read": [_P, ctypes.c_size_t, _P, _P],
     "qe_set_tuning": [ctypes.c_char_p, _I],
+    "qe_gemm_reserve_workspace": [_P],
 }
 
 ENGINE_SIGNATURES = {
@@ -463,6 +464,10 @@ class Engine:
 def stream_read(data, nbytes: int, sink, stream=None):
     """Streaming-read kernel (qe_stream_read): bandwidth ceiling / counter calibration."""
     _call("qe_stream_read", _ptr(data), nbytes, _ptr(sink), _stream(stream))
+
+
+def gemm_reserve_workspace(stream=None):
+    _check(lib().qe_gemm_reserve_workspace(_stream(stream)), "qe_gemm_reserve_workspace")
 
 
 def set_tuning(key: str, value: int):

@@ -68,23 +68,50 @@ def test_engine_rejects_bad_config_on_host():
     assert "unsupported" in qe_amd.lib().qe_last_error().decode()
 
 
-def test_cpp_mirror_header_compiles(tmp_path):
-    """include/kernels.hpp (the reference-named C++ API) compiles against the C-ABI."""
+def test_cpp_mirror_header_compiles():
+    """include/kernels.hpp (the reference-named C++ API) compiles every launcher
+    call of the reference's decode and prefill loops (src/engine.cu:361-580),
+    with the default arguments those calls rely on."""
     import shutil
     import subprocess
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(hipcc):
         pytest.skip("hipcc not available")
-    src = tmp_path / "use.cpp"
-    src.write_text(
-        '#include "kernels.hpp"\n'
-        "void f(const uint32_t* w, const half* s, const int8_t* q, const float* xs, const int32_t* s8,\n"
-        "       half* y, hipStream_t st) {\n"
-        "  qwen::launch_gemv_w4a8(w, s, q, xs, s8, y, y, qwen::HIDDEN_SIZE, qwen::Q_DIM, st);\n"
-        "  qwen::QKVProjectionView v{w, s, y, w, s, y, w, s, y};\n"
-        "  qwen::launch_gemv_qkv_w4a8(v, q, xs, s8, st);\n"
-        "  qwen::launch_gemm_prefill_dual_gate_up_swiglu_w4a16(w, s, y, y, 128, st);\n"
-        "}\n")
+    src = os.path.join(ROOT, "tests", "cpp", "engine_call_shapes.cpp")
     r = subprocess.run([hipcc, "-std=c++20", "-fsyntax-only", "-x", "hip", "--offload-arch=gfx950",
-                        f"-I{ROOT}/include", str(src)], capture_output=True, text=True)
+                        f"-I{ROOT}/include", src], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_cpp_mirror_covers_engine_launchers():
+    """Every launcher that the reference declares in include/kernels.cuh and its
+    engine calls has a namespace-qwen wrapper of the same name."""
+    text = open(os.path.join(ROOT, "include", "kernels.hpp")).read()
+    names = set(re.findall(r"^inline void (launch_\w+)\(", text, re.M))
+    engine_calls = {
+        "launch_embed_lookup_w4a16", "launch_rmsnorm_fp16", "launch_rmsnorm_q8_1", "launch_quantize_fp16_to_q8_1",
+        "launch_gemv_w4a16", "launch_gemv_w4a8", "launch_gemv_qkv_w4a8", "launch_gemv_dual_gate_up_swiglu_w4a16",
+        "launch_gemv_dual_gate_up_swiglu_w4a8", "launch_gemm_prefill_w4a16", "launch_gemm_prefill_qkv_w4a16",
+        "launch_gemm_prefill_dual_gate_up_swiglu_w4a16", "launch_qkv_bias_rope_kv_append",
+        "launch_attention_gqa_flash_decode", "launch_attention_gqa_prefill", "launch_sample_and_advance",
+    }
+    assert engine_calls <= names, engine_calls - names
+
+
+def test_cpp_wrappers_throw(tmp_path):
+    """A program linked against libqe_amd.so through kernels.hpp gets a
+    std::runtime_error for a rejected launch (host-side check, no GPU)."""
+    import shutil
+    import subprocess
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    lib = os.path.join(ROOT, "qwen-engine_amd", "libqe_amd.so")
+    if not os.path.exists(hipcc) or not os.path.exists(lib):
+        pytest.skip("hipcc or the built library not available")
+    exe = tmp_path / "throws"
+    r = subprocess.run([hipcc, "-std=c++20", "-x", "hip", "--offload-arch=gfx950", f"-I{ROOT}/include",
+                        os.path.join(ROOT, "tests", "cpp", "throws_on_bad_shape.cpp"), "-o", str(exe),
+                        f"-L{os.path.dirname(lib)}", "-lqe_amd", f"-Wl,-rpath,{os.path.dirname(lib)}"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr

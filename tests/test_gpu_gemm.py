@@ -266,3 +266,61 @@ def test_gemm_w4a8_residual_qkv_swiglu(qe, orc):
     for m in rows:
         ref, ex, bd = orc.gemv_swiglu_w4a8(qgu, sgu, hq[m], hx[m], hs[m], H, I)
         assert_fp16_close(host(mlp)[m], ex, bd, ref, what="gemm_w4a8 swiglu")
+
+
+def test_gemm_split_k_streams_do_not_share_partials(qe, orc):
+    """Two split-K GEMMs in flight on two streams at once give the results
+    each gives alone: every stream has its own workspace for the partials."""
+    M, H, I = 128, 1536, 8960
+    qa, sa = orc.synth_w4(41, 2 * I, H)
+    qb, sb = orc.synth_w4(42, H, I)
+    A1, A2 = _A(orc, M, H, 43), _A(orc, M, I, 44)
+    dqa, dsa, dqb, dsb, dA1, dA2 = dev(qa), dev(sa), dev(qb), dev(sb), dev(A1), dev(A2)
+    alone = []
+    for fn in (lambda o, s: qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a16(dqa, dsa, dA1, o, M, stream=s,
+                                                                            hidden_size=H, intermediate_size=I),
+               lambda o, s: qe.launch_gemm_prefill_w4a16(dqb, dsb, dA2, None, o, M, H, I, stream=s)):
+        o = empty((M, I if len(alone) == 0 else H), torch.float16)
+        fn(o, None)
+        alone.append(host(o))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        o1, o2 = empty((M, I), torch.float16), empty((M, H), torch.float16)
+        torch.cuda.synchronize()
+        for rep in range(4):  # interleave the launches so the two streams overlap
+            qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a16(dqa, dsa, dA1, o1, M, stream=s1, hidden_size=H,
+                                                             intermediate_size=I)
+            qe.launch_gemm_prefill_w4a16(dqb, dsb, dA2, None, o2, M, H, I, stream=s2)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(o1).view(np.uint16), alone[0].view(np.uint16))
+        assert np.array_equal(host(o2).view(np.uint16), alone[1].view(np.uint16))
+    ref, ex, bd = orc.gemm_w4a16(qb, sb, A2[:8], 8, H, I)
+    assert_fp16_close(alone[1][:8], ex, bd, ref, what="down M=128 rows 0..7")
+
+
+def test_gemm_captured_without_workspace_matches_tolerance(qe, orc):
+    """A GEMM captured into a graph on a stream that never ran one eagerly has
+    no workspace (no allocation under capture) and runs without K slices;
+    after qe_gemm_reserve_workspace it splits again.  Both stay within the
+    oracle tolerance and replays repeat bit for bit."""
+    M, N, K = 128, 1536, 8960
+    qw, sc = orc.synth_w4(51, N, K)
+    A = _A(orc, M, K, 52)
+    dq, ds, dA = dev(qw), dev(sc), dev(A)
+    ref, ex, bd = orc.gemm_w4a16(qw, sc, A[:16], 16, N, K)
+    for reserve in (False, True):
+        s = torch.cuda.Stream()
+        if reserve:
+            qe.gemm_reserve_workspace(s)
+        out = empty((M, N), torch.float16)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            qe.launch_gemm_prefill_w4a16(dq, ds, dA, None, out, M, N, K)
+        outs = []
+        for _ in range(3):
+            out.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            outs.append(host(out).copy())
+        assert all(np.array_equal(o.view(np.uint16), outs[0].view(np.uint16)) for o in outs)
+        assert_fp16_close(outs[0][:16], ex, bd, ref, what=f"captured gemm reserve={reserve}")
