@@ -155,6 +155,21 @@ int qe_launch_gemm_prefill_w4a16(const uint32_t* qweight, const uint16_t* scales
                                  const uint16_t* residual, uint16_t* output_y, int M, int N, int K,
                                  hipStream_t stream, int sm_count);
 
+/* qe_launch_gemm_prefill_w4a16 without any allocation, for callers that
+ * cannot allocate (code under graph capture on a stream with no workspace,
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  Same arguments, same tile and K-slice plan and same results as
+ * qe_launch_gemm_prefill_w4a16; the split-K partials go to a 32 MiB device
+ * array of the library (one per GPU, held until the process ends) instead of
+ * the stream's workspace.  Rejects M * N > 8388608 (QE_ERR_INVALID_ARGUMENT).
+ * Every call on one GPU shares that array: calls that overlap in time on one
+ * GPU (different streams, no ordering between them) race and give wrong
+ * results.  Calls ordered on one stream are safe; nothing needs clearing
+ * between calls (each slice writes its partials before they are read). */
+int qe_launch_gemm_prefill_w4a16_noalloc(const uint32_t* qweight, const uint16_t* scales, const uint16_t* input_x,
+                                         const uint16_t* residual, uint16_t* output_y, int M, int N, int K,
+                                         hipStream_t stream, int sm_count);
+
 /* Replaces launch_gemm_prefill_qkv_w4a16, include/kernels.cuh:132-142. */
 int qe_launch_gemm_prefill_qkv_w4a16(const qe_qkv_view* view, const uint16_t* input_x, int M,
                                      hipStream_t stream, int in_features, int num_q_heads,

@@ -911,6 +911,28 @@ extern "C" int qe_gemm_reserve_workspace(hipStream_t stream) {
 namespace qe {
 namespace {
 
+// Scratch of the allocation-free entry point: a file-scope device array of
+// the same capacity as a stream's workspace, so that entry point makes the
+// same tile and K-slice plan as qe_launch_gemm_prefill_w4a16.  Its device
+// address comes from hipGetSymbolAddress, once per device; host code uses
+// only that address (the array's name is not a device address on the host).
+__device__ __align__(256) float scratch[kWsFloats];
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[64];
+
+float* scratch_address(int dev) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = static_cast<float*>(ptr);
+    }
+    return g_scratch_ptr[dev];
+}
+
 int check_gemm_common(const char* what, const uint16_t* A, int M, int K) {
     QE_REQUIRE(A != nullptr, "%s: input_x is NULL", what);
     QE_REQUIRE(M >= 0, "%s: M=%d", what, M);
@@ -944,6 +966,41 @@ extern "C" int qe_launch_gemm_prefill_w4a16(const uint32_t* qweight, const uint1
     p.N = N;
     p.K = K;
     return launch_gemm<kPlain>(p, stream, what, gemm_workspace(stream), kWsFloats);
+}
+
+extern "C" int qe_launch_gemm_prefill_w4a16_noalloc(const uint32_t* qweight, const uint16_t* scales,
+                                                    const uint16_t* input_x, const uint16_t* residual,
+                                                    uint16_t* output_y, int M, int N, int K, hipStream_t stream,
+                                                    int sm_count) {
+    (void)sm_count;
+    const char* what = "gemm_prefill_w4a16_noalloc";
+    if (int rc = check_gemm_common(what, input_x, M, K)) return rc;
+    QE_REQUIRE(qweight && scales && output_y, "%s: NULL weight/scale/output", what);
+    QE_REQUIRE(N >= 0, "%s: N=%d", what, N);
+    QE_REQUIRE(aligned(qweight, 16) && aligned(scales, 2), "%s: qweight must be 16-byte aligned", what);
+    // the largest shape whose K-slice plan this entry point accepts: one
+    // fp32 partial tile set of M x N per slice must fit the scratch at least
+    // once (larger shapes are rejected rather than silently left unsplit)
+    QE_REQUIRE(static_cast<size_t>(M) * static_cast<size_t>(N) <= kWsFloats,
+               "%s: M*N=%zu exceeds the scratch of %zu floats", what,
+               static_cast<size_t>(M) * static_cast<size_t>(N), kWsFloats);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return fail(QE_ERR_HIP, "%s: no current device", what);
+    float* ws = gemm_split_k_enabled() ? scratch_address(dev) : nullptr;
+    if (gemm_split_k_enabled() && ws == nullptr)
+        return fail(QE_ERR_HIP, "%s: hipGetSymbolAddress(scratch) failed", what);
+    GemmParams p{};
+    p.qw[0] = qweight;
+    p.sc[0] = scales;
+    p.out[0] = output_y;
+    p.out_stride[0] = N;
+    p.A = input_x;
+    p.residual = residual;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    return launch_gemm<kPlain>(p, stream, what, ws, kWsFloats);
 }
 
 extern "C" int qe_launch_gemm_prefill_qkv_w4a16(const qe_qkv_view* view, const uint16_t* input_x, int M,

@@ -32,6 +32,7 @@ SIGNATURES = {
     "qe_launch_gemv_w4a16": [_P, _P, _P, _P, _P, _I, _I, _P],
     "qe_launch_gemv_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _I, _I, _P],
     "qe_launch_gemm_prefill_w4a16": [_P, _P, _P, _P, _P, _I, _I, _I, _P, _I],
+    "qe_launch_gemm_prefill_w4a16_noalloc": [_P, _P, _P, _P, _P, _I, _I, _I, _P, _I],
     "qe_launch_gemm_prefill_qkv_w4a16": [_P, _P, _I, _P, _I, _I, _I, _I, _I],
     "qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _I, _P, _I, _I],
     "qe_launch_sample_and_advance": [_P, _P, _P, _P, _P, _P, _I],
@@ -201,6 +202,12 @@ def launch_gemv_dual_gate_up_swiglu_w4a16(gate_up_qweight, gate_up_scales, input
 
 def launch_gemm_prefill_w4a16(qweight, scales, input_x, residual, output_y, M, N, K, stream=None, sm_count=0):
     _call("qe_launch_gemm_prefill_w4a16", _ptr(qweight), _ptr(scales), _ptr(input_x), _ptr(residual),
+          _ptr(output_y), M, N, K, _stream(stream), sm_count)
+
+
+def launch_gemm_prefill_w4a16_noalloc(qweight, scales, input_x, residual, output_y, M, N, K, stream=None,
+                                      sm_count=0):
+    _call("qe_launch_gemm_prefill_w4a16_noalloc", _ptr(qweight), _ptr(scales), _ptr(input_x), _ptr(residual),
           _ptr(output_y), M, N, K, _stream(stream), sm_count)
 
 
