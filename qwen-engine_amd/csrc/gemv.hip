@@ -29,6 +29,7 @@
 #include <algorithm>
 
 #include "attn_common.hpp"
+#include "rms_common.hpp"
 #include "rope_common.hpp"
 #include "sample_common.hpp"
 
@@ -100,21 +101,6 @@ struct GemvParams {
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-template <int BT>
-__device__ __forceinline__ float block_sum(float v, float* s_red) {
-    v = qwen::seg_sum<64>(v);
-    if constexpr (BT == 64) {
-        return v;
-    } else {
-        if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
-        __syncthreads();
-        float t = 0.0f;
-#pragma unroll
-        for (int w = 0; w < BT / 64; ++w) t += s_red[w];
-        return t;
-    }
-}
-
 __device__ __forceinline__ void unpack8(const uint4 raw, float vals[8]) {
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
@@ -151,8 +137,10 @@ __device__ __forceinline__ uint4 rms_apply8(uint4 xv, uint4 gv, _Float16 h) {
 // Stage the activation of the whole block in LDS: s_q8[K] and, per
 // 32-element chunk, s_rec[c] = {sum8[4c..4c+3] summed, bits of x_scale}.
 // VEC: 16-byte vector loads are legal for the activation buffers.
+// kXRMS: s_units holds K / 8 floats for the sum of squares.
 template <int XM, int BT, bool VEC>
-__device__ __forceinline__ void stage_activation(const GemvParams& p, int8_t* s_q8, int2* s_rec, float* s_red) {
+__device__ __forceinline__ void stage_activation(const GemvParams& p, int8_t* s_q8, int2* s_rec, float* s_red,
+                                                 float* s_units) {
     const int K = p.K;
     const int G = K >> 7;
     if constexpr (XM == kXQ8) {
@@ -169,15 +157,8 @@ __device__ __forceinline__ void stage_activation(const GemvParams& p, int8_t* s_
     } else {
         _Float16 h = static_cast<_Float16>(0.0f);
         if constexpr (XM == kXRMS) {
-            float ss = 0.0f;
-            for (int i = threadIdx.x; i < (K >> 3); i += BT) {
-                float v[8];
-                unpack8(load8_f16(p.x16 + 8 * i, VEC), v);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
-            }
-            const float total = block_sum<BT>(ss, s_red);
-            h = static_cast<_Float16>(1.0f / sqrtf(total / static_cast<float>(K) + kRmsEps));
+            for (int i = threadIdx.x; i < (K >> 3); i += BT) s_units[i] = rms_unit_sq(load8_f16(p.x16 + 8 * i, VEC));
+            h = rms_inv_f16(s_units, K >> 3, K, kRmsEps, s_red);
         }
         const int sub = threadIdx.x & 15;
         for (int g = threadIdx.x >> 4; g < G; g += BT / 16) {
@@ -341,23 +322,15 @@ __device__ __forceinline__ void stage_issue_f16(const GemvParams& p, uint4 (&raw
 
 template <int XM, int BT, int MAXP>
 __device__ __forceinline__ void stage_finish_f16(const GemvParams& p, uint4 (&raw)[MAXP], const uint4 (&graw)[MAXP],
-                                                 int8_t* s_q8, int2* s_rec, float* s_red) {
+                                                 int8_t* s_q8, int2* s_rec, float* s_red, float* s_units) {
     const int K = p.K;
     const int U = K >> 3;  // 8-element units
     const int t = threadIdx.x;
     if constexpr (XM == kXRMS) {
-        float ss = 0.0f;
 #pragma unroll
-        for (int j = 0; j < MAXP; ++j) {
-            float v[8];
-            unpack8(raw[j], v);
-            float sj = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sj += v[e] * v[e];
-            ss += (t + BT * j < U) ? sj : 0.0f;
-        }
-        const float total = block_sum<BT>(ss, s_red);
-        const _Float16 h = static_cast<_Float16>(1.0f / sqrtf(total / static_cast<float>(K) + kRmsEps));
+        for (int j = 0; j < MAXP; ++j)
+            if (t + BT * j < U) s_units[t + BT * j] = rms_unit_sq(raw[j]);
+        const _Float16 h = rms_inv_f16(s_units, U, K, kRmsEps, s_red);
         const bool write_norm = p.norm_out != nullptr && blockIdx.x == 0;
 #pragma unroll
         for (int j = 0; j < MAXP; ++j) {
@@ -603,7 +576,8 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
         int2* s_rec = reinterpret_cast<int2*>(s_mem + K);
         if constexpr (XM == kXQ8) stage_finish_q8<BT, MQ>(p, qa, qb, qs4, qxd, s_q8, s_rec);
         else if constexpr (is_attn(XM)) stage_finish_attn<LS>(p, apo, apl, s_q8, s_rec);
-        else stage_finish_f16<XM, BT, MAXP>(p, raw, graw, s_q8, s_rec, s_red);
+        else stage_finish_f16<XM, BT, MAXP>(p, raw, graw, s_q8, s_rec, s_red,
+                                            reinterpret_cast<float*>(s_mem + K + (K >> 5) * 8 + 32));
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < NCH; ++i) {
@@ -777,7 +751,7 @@ __global__ __launch_bounds__(256) void gemv_w4_generic_kernel(GemvParams p) {
     const int KW = K >> 3;
     int8_t* s_q8 = reinterpret_cast<int8_t*>(s_mem);
     int2* s_rec = reinterpret_cast<int2*>(s_mem + K);
-    stage_activation<XM, 256, false>(p, s_q8, s_rec, s_red);
+    stage_activation<XM, 256, false>(p, s_q8, s_rec, s_red, reinterpret_cast<float*>(s_mem + K + (K >> 5) * 8));
     __syncthreads();
     const int wave = threadIdx.x >> 6;
     const int l = threadIdx.x & 63;
@@ -860,7 +834,8 @@ int launch_fast(const GemvParams& p, hipStream_t s) {
     if constexpr (XM == kXF16 || XM == kXRMS) cap = std::min(cap, 3 * cu_count());
     if (const int f = gemv_forced_cap()) cap = f;
     if (MODE == kSample && cap > QE_LM_HEAD_SAMPLE_PARTS) cap = QE_LM_HEAD_SAMPLE_PARTS;
-    const size_t lds = static_cast<size_t>(p.K) + (p.K >> 5) * 8 + 32;  // + dummy slot
+    // q8, chunk records + dummy slot, and (RMSNorm) the unit sums of squares
+    const size_t lds = static_cast<size_t>(p.K) + (p.K >> 5) * 8 + 32 + (XM == kXRMS ? (p.K >> 3) * 4 : 0);
     if (grid > cap) {
         gemv_w4_kernel<BT, LPR, NCH, RPS, MODE, XM, true><<<cap, BT, lds, s>>>(p);
         return cap;
@@ -926,7 +901,7 @@ int launch_gemv(GemvParams& p, bool fast_ok, hipStream_t stream, const char* wha
     const int n_out = (MODE == kSwiglu) ? p.n_rows / 2 : p.n_rows;
     int grid = (n_out + 3) / 4;
     if (grid > cu_count() * 8) grid = cu_count() * 8;
-    const size_t lds = static_cast<size_t>(K) + (K >> 5) * 8;
+    const size_t lds = static_cast<size_t>(K) + (K >> 5) * 8 + (XM == kXRMS ? (K >> 3) * 4 : 0);
     gemv_w4_generic_kernel<MODE, XM><<<grid, 256, lds, stream>>>(p);
     return check_launch(what);
 }

@@ -5,6 +5,7 @@
 // (tests/test_kernels.cu:311-326).  These kernels move a few KB and are
 // launch-latency bound; they are written to finish in one wave of blocks.
 #include "qe_common.hpp"
+#include "rms_common.hpp"
 
 namespace qe {
 namespace {
@@ -32,35 +33,15 @@ __global__ __launch_bounds__(256) void quantize_fp16_to_q8_1_kernel(
     if (scale && sub == 0) scale[group] = g.d;
 }
 
-// Block-wide sum for 256 threads (4 waves): DPP/swizzle inside the wave,
-// LDS across waves.  Every thread returns the total.
-__device__ __forceinline__ float block_sum_256(float v, float* s_part) {
-    v = qwen::seg_sum<64>(v);
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) s_part[wave] = v;
-    __syncthreads();
-    float t = s_part[0] + s_part[1] + s_part[2] + s_part[3];
-    return t;
-}
-
-// inv_rms = 1/sqrt(mean(x^2) + eps) in fp32; the normalized value is
-// fp16(fp16(x * fp16(inv_rms)) * gamma), the two fp16 multiplies of
-// rmsnorm_rope.cu:130-136 / :214-227.
-__device__ __forceinline__ _Float16 inv_rms_f16(const uint16_t* __restrict__ xr, int H, float eps, float* s_part) {
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < H / 8; i += blockDim.x) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(xr + i * 8);
-        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float a = h2f(static_cast<uint16_t>(w[j] & 0xFFFFu));
-            float b = h2f(static_cast<uint16_t>(w[j] >> 16));
-            ss += a * a + b * b;
-        }
-    }
-    const float total = block_sum_256(ss, s_part);
-    const float inv_rms = 1.0f / sqrtf(total / static_cast<float>(H) + eps);
-    return static_cast<_Float16>(inv_rms);
+// inv_rms = 1/sqrt(mean(x^2) + eps) in fp32 with the shared summation order
+// (rms_common.hpp); the normalized value is fp16(fp16(x * fp16(inv_rms)) *
+// gamma), the two fp16 multiplies of rmsnorm_rope.cu:130-136 / :214-227.
+// s_units: H / 8 floats of LDS.
+__device__ __forceinline__ _Float16 inv_rms_f16(const uint16_t* __restrict__ xr, int H, float eps, float* s_units,
+                                                float* s_total) {
+    for (int i = threadIdx.x; i < H / 8; i += blockDim.x)
+        s_units[i] = rms_unit_sq(*reinterpret_cast<const uint4*>(xr + i * 8));
+    return rms_inv_f16(s_units, H / 8, H, eps, s_total);
 }
 
 __device__ __forceinline__ uint4 norm8(uint4 xv, uint4 gv, _Float16 h) {
@@ -81,10 +62,11 @@ __device__ __forceinline__ uint4 norm8(uint4 xv, uint4 gv, _Float16 h) {
 
 __global__ __launch_bounds__(256) void rmsnorm_fp16_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma, uint16_t* __restrict__ out, int H, float eps) {
-    __shared__ float s_part[4];
+    extern __shared__ __align__(16) float s_units[];  // H / 8
+    __shared__ float s_total;
     const uint16_t* xr = x + static_cast<size_t>(blockIdx.x) * H;
     uint16_t* orow = out + static_cast<size_t>(blockIdx.x) * H;
-    const _Float16 h = inv_rms_f16(xr, H, eps, s_part);
+    const _Float16 h = inv_rms_f16(xr, H, eps, s_units, &s_total);
     for (int i = threadIdx.x; i < H / 8; i += blockDim.x) {
         const uint4 xv = *reinterpret_cast<const uint4*>(xr + i * 8);
         const uint4 gv = *reinterpret_cast<const uint4*>(gamma + i * 8);
@@ -93,13 +75,17 @@ __global__ __launch_bounds__(256) void rmsnorm_fp16_kernel(
 }
 
 // One token: RMSNorm into LDS (and optionally HBM), then Q8_1 of the
-// fp16-rounded normalized values.  Dynamic LDS: H fp16.
+// fp16-rounded normalized values.  Dynamic LDS: H fp16 (2H bytes, at most
+// 128 KiB).  The unit sums of squares (H / 8 floats) use the same LDS: they
+// are dead once rms_inv_f16 returns (its second barrier follows the last
+// read), before the first normalized value is stored.
 __global__ __launch_bounds__(256) void rmsnorm_q8_1_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma, uint16_t* out_opt,
     int8_t* __restrict__ q8, float* __restrict__ scale, int32_t* __restrict__ sum8, int H, float eps) {
     extern __shared__ __align__(16) uint16_t s_norm[];
-    __shared__ float s_part[4];
-    const _Float16 h = inv_rms_f16(x, H, eps, s_part);
+    __shared__ float s_total;
+    float* s_units = reinterpret_cast<float*>(s_norm);
+    const _Float16 h = inv_rms_f16(x, H, eps, s_units, &s_total);
     for (int i = threadIdx.x; i < H / 8; i += blockDim.x) {
         const uint4 xv = *reinterpret_cast<const uint4*>(x + i * 8);
         const uint4 gv = *reinterpret_cast<const uint4*>(gamma + i * 8);
@@ -162,11 +148,12 @@ extern "C" int qe_launch_rmsnorm_q8_1(const uint16_t* input, const uint16_t* gam
 extern "C" int qe_launch_rmsnorm_fp16(const uint16_t* input, const uint16_t* gamma, uint16_t* output,
                                       int num_tokens, hipStream_t stream, int hidden_size) {
     QE_REQUIRE(input && gamma && output, "rmsnorm_fp16: NULL pointer");
-    QE_REQUIRE(hidden_size > 0 && hidden_size % 8 == 0, "rmsnorm_fp16: hidden_size=%d must be a multiple of 8",
-               hidden_size);
+    QE_REQUIRE(hidden_size > 0 && hidden_size % 8 == 0 && hidden_size <= 65536,
+               "rmsnorm_fp16: hidden_size=%d must be a positive multiple of 8 (<= 65536)", hidden_size);
     QE_REQUIRE(aligned(input, 16) && aligned(gamma, 16) && aligned(output, 16),
                "rmsnorm_fp16: buffers must be 16-byte aligned");
     if (num_tokens <= 0) return QE_OK;
-    rmsnorm_fp16_kernel<<<num_tokens, 256, 0, stream>>>(input, gamma, output, hidden_size, kRmsEps);
+    rmsnorm_fp16_kernel<<<num_tokens, 256, hidden_size / 8 * sizeof(float), stream>>>(input, gamma, output,
+                                                                                       hidden_size, kRmsEps);
     return check_launch("rmsnorm_fp16");
 }

@@ -187,15 +187,20 @@ def test_fused_rmsnorm_qkv(qe, orc, H):
     view2 = qe.make_qkv_view(dw[0][0], dw[0][1], outs2[0], dw[1][0], dw[1][1], outs2[1], dw[2][0], dw[2][1], outs2[2])
     qe.launch_gemv_qkv_w4a8(view2, q8, sc, s8, in_features=H, num_q_heads=nq, num_kv_heads=nkv, head_dim=hd)
     n_gpu = host(norm)
+    # one summation order for the sum of squares in every RMSNorm kernel: the
+    # fused prologue and rmsnorm_q8_1 give the same normalized vector, Q8_1
+    # and projections, bit for bit
+    assert np.array_equal(n_gpu.view(np.uint16), host(norm2).view(np.uint16))
     from helpers import ulp16
-    # both kernels reduce the sum of squares in their own order: 1 ulp at most
-    assert np.all(np.abs(n_gpu.astype(np.float64) - host(norm2).astype(np.float64)) <= ulp16(n_gpu))
+    n_ref = orc.rmsnorm_fp16(x16, g16)
+    assert np.all(np.abs(n_gpu.astype(np.float64) - n_ref.astype(np.float64)) <= ulp16(n_ref))
     # oracle on the normalized vector the kernel produced
     rq, rs, rs8 = orc.quantize_q8_1(n_gpu)
+    assert np.array_equal(host(q8), rq) and np.array_equal(host(s8), rs8)
     for (w, s), f, o2, n in zip(mats, fused, outs2, dims):
         ref, ex, bd = orc.gemv_w4a8(w, s, rq, rs, rs8, n, H)
         assert_fp16_close(f, ex, bd, ref, what="fused qkv")
-        assert_fp16_close(host(o2), ex, bd, ref, what="two-launch qkv")
+        assert np.array_equal(f.view(np.uint16), host(o2).view(np.uint16))
 
 
 @pytest.mark.parametrize("H,I", [(1536, 8960), (256, 300)])
@@ -212,6 +217,13 @@ def test_fused_rmsnorm_gate_up(qe, orc, H, I):
     assert np.all(np.abs(n_gpu.astype(np.float64) - n_ref.astype(np.float64)) <= ulp16(n_ref))
     ref, ex, bd = orc.gemv_swiglu_w4a16(qw, sc, n_gpu, H, I)
     assert_fp16_close(host(out), ex, bd, ref, what="fused gate_up")
+    # bit-identical to the reference's two launches (src/engine.cu:414-424)
+    q8, xs, s8 = empty(H, torch.int8), empty(H // 128, torch.float32), empty(H // 8, torch.int32)
+    norm2, out2 = empty(H, torch.float16), empty(I, torch.float16)
+    qe.launch_rmsnorm_q8_1(dev(x16), dev(g16), norm2, q8, xs, s8, hidden_size=H)
+    qe.launch_gemv_dual_gate_up_swiglu_w4a8(dev(qw), dev(sc), q8, xs, s8, out2, H, I)
+    assert np.array_equal(n_gpu.view(np.uint16), host(norm2).view(np.uint16))
+    assert np.array_equal(host(out).view(np.uint16), host(out2).view(np.uint16))
 
 
 def test_gemv_w4a16_residual_inplace_down(qe, orc):

@@ -128,3 +128,30 @@ def test_rmsnorm_fp16_rows(qe, orc):
     d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
     assert np.all(d <= ulp_or_zero(ref))
     assert np.mean(got == ref) > 0.99
+
+
+@pytest.mark.parametrize("H", [128, 1536, 8960, 65536])
+def test_rmsnorm_kernels_agree_bit_for_bit(qe, orc, H):
+    """rmsnorm_fp16 (prefill), rmsnorm_q8_1 (decode) and the fused RMSNorm GEMV
+    prologue sum the squares in one shared order: the same row gives the same
+    normalized fp16 vector in all of them."""
+    rng = np.random.default_rng(H)
+    x16 = (rng.standard_normal((3, H)) * np.array([[0.01], [1.0], [40.0]])).astype(np.float16)
+    g16 = (1 + 0.2 * rng.standard_normal(H)).astype(np.float16)
+    rows = empty((3, H), torch.float16)
+    qe.launch_rmsnorm_fp16(dev(x16), dev(g16), rows, 3, hidden_size=H)
+    a = host(rows)
+    for t in range(3):
+        out = empty(H, torch.float16)
+        q8, sc, s8 = empty(H, torch.int8), empty(H // 128, torch.float32), empty(H // 8, torch.int32)
+        qe.launch_rmsnorm_q8_1(dev(x16[t]), dev(g16), out, q8, sc, s8, hidden_size=H)
+        assert np.array_equal(host(out).view(np.uint16), a[t].view(np.uint16)), t
+        if H <= 16384:
+            norm = empty(H, torch.float16)
+            qw, wsc = orc.synth_w4(H, 256, H)
+            mlp = empty(128, torch.float16)
+            qe.launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(dev(x16[t]), dev(g16), norm, dev(qw), dev(wsc), mlp, H,
+                                                             128)
+            assert np.array_equal(host(norm).view(np.uint16), a[t].view(np.uint16)), t
+    ref = orc.rmsnorm_fp16(x16, g16)
+    assert np.all(np.abs(a.astype(np.float64) - ref.astype(np.float64)) <= ulp_or_zero(ref))
