@@ -117,30 +117,8 @@ __global__ __launch_bounds__(256) void qkv_bias_rope_kv_append_kernel(
 // Output per (q head, split): unnormalized o relative to the split max m, and
 // (m, denominator) with m in natural-log units, as attention_gqa.cu's stage 1
 // writes them.
-//
-// QE_S1_TIMING=1 builds a timing probe: block-level timestamps of each phase
-// (s_memrealtime, 100 MHz) into g_dbg_ts, read back with qe_debug_ts.
-#ifndef QE_FLASH_NT
-#define QE_FLASH_NT 512
-#endif
-#if QE_S1_TIMING
-__device__ unsigned long long g_dbg_ts[256][8];
-#define QE_TS(i, wait)                                                                                  \
-    do {                                                                                                \
-        if (wait) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");                          \
-        __builtin_amdgcn_sched_barrier(0);                                                              \
-        const unsigned long long t_ = __builtin_amdgcn_s_memrealtime();                                 \
-        if (threadIdx.x == 0) g_dbg_ts[blockIdx.y * gridDim.x + blockIdx.x][i] = t_;                     \
-        __builtin_amdgcn_sched_barrier(0);                                                              \
-    } while (0)
-#define QE_TS_ZERO(i) \
-    if (threadIdx.x == 0) g_dbg_ts[blockIdx.y * gridDim.x + blockIdx.x][i] = 0
-#else
-#define QE_TS_ZERO(i)
-#define QE_TS(i, wait) \
-    do {               \
-    } while (0)
-#endif
+
+constexpr int kFlashThreads = 512;  // stage-1 block: two blocks per kv head, half a GQA group each
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
@@ -229,7 +207,6 @@ __device__ __forceinline__ void flash_decode_split(const uint16_t* __restrict__ 
             vr[st] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vc + base + static_cast<size_t>(t) * kHeadDim));
         }
     };
-    QE_TS(2, true);
     FlashState<GH> S;
 #pragma unroll
     for (int h = 0; h < GH; ++h) {
@@ -255,7 +232,6 @@ __device__ __forceinline__ void flash_decode_split(const uint16_t* __restrict__ 
             if (r0 >= t1) break;
         }
     }
-    QE_TS(3, false);
     // merge the NG lane-group states through LDS, HP heads per pass (48 KB):
     // M = max_g m_g, w_g = exp2(m_g - M), L = sum_g l_g w_g, o = sum_g w_g o_g
     constexpr int HP = (GH * NG <= 96) ? GH : 96 / NG;
@@ -322,8 +298,6 @@ __device__ __forceinline__ void flash_decode_split(const uint16_t* __restrict__ 
             }
         }
     }
-    QE_TS(5, false);
-    QE_TS(6, true);
 }
 
 // grid (num_kv_heads * group / GH, kSplits): block x covers q heads
@@ -340,8 +314,6 @@ __global__ __launch_bounds__(NT) void flash_decode_stage1_kernel(const uint16_t*
     const int qh0 = blockIdx.x * GH, split = blockIdx.y;
     const int kvh = qh0 / group;
     const int gid = threadIdx.x >> 4, j = threadIdx.x & 15;
-    QE_TS(7, false);
-    QE_TS(0, false);
     // q and the split's first 64 rows are requested before the position is
     // known: with splits of 64 positions (contexts up to 16 * 64) the rows are
     // those of split * 64 onwards; rows past the context are masked later
@@ -364,9 +336,7 @@ __global__ __launch_bounds__(NT) void flash_decode_stage1_kernel(const uint16_t*
     const int per = flash_split_len(seq_len);
     const int t0 = split * per;
     const int t1 = min(t0 + per, seq_len);
-    QE_TS(1, true);
     if (t0 >= t1) {
-        QE_TS_ZERO(6);
         if (threadIdx.x < GH) {
             const size_t li = (static_cast<size_t>(qh0 + threadIdx.x) * kSplits + split) * 2;
             part_lse[li] = -INFINITY;
@@ -672,7 +642,7 @@ int launch_flash_stage1(const uint16_t* q, const uint16_t* kc, const uint16_t* v
     QE_REQUIRE(max_seq_len > 0, "%s: max_seq_len=%d", what, max_seq_len);
     // q heads per block: half of a kv head's group (two blocks per kv head)
     const dim3 grid2(num_q_heads / (group > 1 ? group / 2 : 1), kSplits);
-    constexpr int NT = QE_FLASH_NT;
+    constexpr int NT = kFlashThreads;
     switch (group) {
         case 1: flash_decode_stage1_kernel<1, NT><<<grid2, NT, 0, stream>>>(q, kc, vc, part_o, part_lse, ctl, group, max_seq_len); break;
         case 2: flash_decode_stage1_kernel<1, NT><<<grid2, NT, 0, stream>>>(q, kc, vc, part_o, part_lse, ctl, group, max_seq_len); break;
@@ -701,11 +671,6 @@ extern "C" int qe_launch_attention_gqa_flash_decode(const uint16_t* q, const uin
     return check_launch("attention_gqa_flash_decode");
 }
 
-#if QE_S1_TIMING
-extern "C" int qe_debug_ts(void* host) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(qe::g_dbg_ts), sizeof(qe::g_dbg_ts)) == hipSuccess ? 0 : 1;
-}
-#endif
 
 extern "C" int qe_launch_attention_gqa_flash_decode_partials(const uint16_t* q, const uint16_t* layer_k_cache,
                                                              const uint16_t* layer_v_cache, float* splitk_partial_out,

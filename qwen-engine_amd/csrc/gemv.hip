@@ -52,24 +52,6 @@ constexpr int kXATTN16 = 5;
 
 constexpr float kRmsEps = 1e-6f;  // RMS_NORM_EPS, include/config.cuh:20
 
-// QE_GEMV_TIMING=1 builds a timing probe: per-block phase timestamps
-// (s_memrealtime, 100 MHz) into g_dbg_gemv, read back with qe_debug_gemv_ts.
-#if QE_GEMV_TIMING
-__device__ unsigned long long g_dbg_gemv[6][4096][8];
-#define QE_GTS(i, wait)                                                                      \
-    do {                                                                                     \
-        if (wait) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");               \
-        __builtin_amdgcn_sched_barrier(0);                                                   \
-        const unsigned long long t_ = __builtin_amdgcn_s_memrealtime();                      \
-        if (threadIdx.x == 0 && blockIdx.x < 4096) g_dbg_gemv[TS_KIND][blockIdx.x][i] = t_; \
-        __builtin_amdgcn_sched_barrier(0);                                                   \
-    } while (0)
-#else
-#define QE_GTS(i, wait) \
-    do {                \
-    } while (0)
-#endif
-
 struct GemvParams {
     const uint32_t* qw[3];
     const uint16_t* sc[3];
@@ -465,10 +447,6 @@ __device__ __forceinline__ int rope_row(int set) {
 
 template <int BT, int LPR, int NCH, int RPS, int MODE, int XM, bool LOOP>
 __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
-#if QE_GEMV_TIMING
-    constexpr int TS_KIND = MODE == kQKV ? 0 : (is_attn(XM) ? 1 : (MODE == kSwiglu ? 2 : (MODE == kSample ? 4 : 3)));
-#endif
-    QE_GTS(7, false);
     // SwiGLU: a segment owns a (gate, up) row pair (RPS 2), or, with 16-lane
     // segments and RPS 1, segments 2s and 2s+1 own the gate and up row and
     // meet through a 32-lane swizzle
@@ -481,7 +459,6 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
     const int l = threadIdx.x % LPR;
     const int n_sets = (p.n_rows + RPS - 1) / RPS;
     const int set_stride = SEGS * gridDim.x;
-    QE_GTS(0, false);
 
     // ---- activation loads first (a few KB, needed first), then the first
     //      row set's weights; the activation math overlaps the weight stream.
@@ -521,13 +498,6 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
         }
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
-#if QE_GEMV_ISSUE_BARRIER
-    // every wave's activation loads are issued before any wave's weight loads:
-    // the staging barrier below waits for the activation of all waves, which
-    // would otherwise queue behind other waves' weight loads
-    if constexpr (BT > 64) __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-#endif
 
     int set = blockIdx.x * SEGS + seg;
     u32x4 w[RPS][NCH];
@@ -556,7 +526,6 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
     };
     load_set(min(set, n_sets - 1), w, hs);
     __builtin_amdgcn_sched_barrier(0);
-    QE_GTS(1, false);
     // QKV with RoPE: position and angle of this lane's row, while the loads
     // are in flight (the bias was requested with the activation, ahead of the
     // weights, so using it does not wait for them)
@@ -677,12 +646,8 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
             }
         }
     };
-    QE_GTS(2, false);
     if constexpr (!LOOP) {
-        QE_GTS(3, true);
         finish_set(set);  // the grid covers every set once
-        QE_GTS(4, false);
-        QE_GTS(5, true);
     } else {
         for (; set < n_sets; set += set_stride) {
             u32x4 wn[RPS][NCH];
@@ -1144,11 +1109,6 @@ extern "C" int qe_launch_attention_combine_gemv_o_w4a8(const float* splitk_parti
     return check_launch(what);
 }
 
-#if QE_GEMV_TIMING
-extern "C" int qe_debug_gemv_ts(void* host) {
-    return hipMemcpyFromSymbol(host, HIP_SYMBOL(qe::g_dbg_gemv), sizeof(qe::g_dbg_gemv)) == hipSuccess ? 0 : 1;
-}
-#endif
 
 // ---- fused LM head + sampling ------------------------------------------------------
 namespace qe {
