@@ -155,8 +155,9 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const f32x16 (&acc
 // of the quad take k = 128h + 32t + 8s in step t, sub-step s.  A step then
 // spans two 32-k pieces of A, 128 k apart.  Without QUAD each step loads
 // 16 bytes per lane (k = 32h + 8s) and one scale.
-template <int BM, int BN, int WGM, int MODE, bool QUAD>
+template <int BM, int BN, int WGM, int MODE, bool QUAD, bool TILED = false>
 __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
+    static_assert(QUAD || !TILED, "the tiled weight layout is read quad by quad");
     constexpr int WGN = 4 / WGM;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int MI = WM / 32, NI = WN / 32;
@@ -207,8 +208,14 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
             m = (col >= p.col_begin[1]) + (col >= p.col_begin[2]);
             local = col - p.col_begin[m];
         }
-        b_src[j] = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(local) * (K >> 3)) + (QUAD ? 4 : 1) * h;
-        b_sc[j] = p.sc[m] + static_cast<size_t>(local) * G + (QUAD ? h : 0);
+        if constexpr (TILED) {
+            const size_t tq = static_cast<size_t>(local >> 5) * (K >> 8);  // first quad of the column tile
+            b_src[j] = reinterpret_cast<const u32x4*>(p.qw[m]) + tq * 256 + 32 * h + (local & 31);
+            b_sc[j] = p.sc[m] + tq * 64 + 32 * h + (local & 31);
+        } else {
+            b_src[j] = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(local) * (K >> 3)) + (QUAD ? 4 : 1) * h;
+            b_sc[j] = p.sc[m] + static_cast<size_t>(local) * G + (QUAD ? h : 0);
+        }
     }
 
     u32x4 ra[D][A_U4];
@@ -225,9 +232,9 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
 #pragma unroll
-            for (int i = 0; i < (QUAD ? 4 : 1); ++i)
-                rb[e][j][i] = b_src[j][QUAD ? 8 * g + i : 2 * g];  // cached: every M tile of the column reads it
-            rs[e][j] = b_sc[j][QUAD ? 2 * g : (g >> 1)];
+            for (int i = 0; i < (QUAD ? 4 : 1); ++i)  // cached: every M tile of the column reads it
+                rb[e][j][i] = TILED ? b_src[j][256 * g + 64 * i] : b_src[j][QUAD ? 8 * g + i : 2 * g];
+            rs[e][j] = TILED ? b_sc[j][64 * g] : b_sc[j][QUAD ? 2 * g : (g >> 1)];
         }
     };
     auto store_a = [&](int buf, int d) __attribute__((always_inline)) {
@@ -357,7 +364,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
 // A through a 4-stage register ring and a double-buffered LDS tile, weights
 // a quad ahead (the group's two 16-byte pieces of each column and quad),
 // the four sub-steps software-pipelined.
-template <int BM, int BN, int WGM, int MODE>
+template <int BM, int BN, int WGM, int MODE, bool TILED = false>
 __global__ __launch_bounds__(512, 1) void gemm_w4a16_ks2_kernel(GemmParams p) {
     constexpr int WGN = 4 / WGM;
     constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -410,8 +417,14 @@ __global__ __launch_bounds__(512, 1) void gemm_w4a16_ks2_kernel(GemmParams p) {
             m = (col >= p.col_begin[1]) + (col >= p.col_begin[2]);
             local = col - p.col_begin[m];
         }
-        b_src[j] = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(local) * (K >> 3)) + 4 * h + kg;
-        b_sc[j] = p.sc[m] + static_cast<size_t>(local) * G + h;
+        if constexpr (TILED) {
+            const size_t tq = static_cast<size_t>(local >> 5) * (K >> 8);
+            b_src[j] = reinterpret_cast<const u32x4*>(p.qw[m]) + tq * 256 + 64 * kg + 32 * h + (local & 31);
+            b_sc[j] = p.sc[m] + tq * 64 + 32 * h + (local & 31);
+        } else {
+            b_src[j] = reinterpret_cast<const u32x4*>(p.qw[m] + static_cast<size_t>(local) * (K >> 3)) + 4 * h + kg;
+            b_sc[j] = p.sc[m] + static_cast<size_t>(local) * G + h;
+        }
     }
 
     u32x4 ra[D][A_U4];
@@ -426,9 +439,9 @@ __global__ __launch_bounds__(512, 1) void gemm_w4a16_ks2_kernel(GemmParams p) {
         const int g = (kt_begin >> 2) + qd;
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
-            rb[e][j][0] = b_src[j][8 * g];
-            rb[e][j][1] = b_src[j][8 * g + 2];
-            rs[e][j] = b_sc[j][2 * g];
+            rb[e][j][0] = TILED ? b_src[j][256 * g] : b_src[j][8 * g];
+            rb[e][j][1] = TILED ? b_src[j][256 * g + 128] : b_src[j][8 * g + 2];
+            rs[e][j] = TILED ? b_sc[j][64 * g] : b_sc[j][2 * g];
         }
     };
     auto store_a = [&](int buf, int d) __attribute__((always_inline)) {
@@ -597,7 +610,7 @@ void launch_reduce(const GemmParams& p, dim3 tiles, int slices, hipStream_t s) {
     }
 }
 
-template <int BM, int BN, int WGM, int MODE>
+template <int BM, int BN, int WGM, int MODE, bool TILED = false>
 void launch_tiles(const GemmParams& p, int slices, hipStream_t s) {
     const dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, slices);
     // two k groups per block when the grid leaves every CU with at most one
@@ -606,13 +619,13 @@ void launch_tiles(const GemmParams& p, int slices, hipStream_t s) {
     const bool two = p.K % 256 == 0 && ks2 != 1 &&
                      (ks2 == 2 || static_cast<long long>(grid.x) * grid.y * grid.z <= cu_count());
     if (two) {
-        gemm_w4a16_ks2_kernel<BM, BN, WGM, MODE><<<grid, 512, 0, s>>>(p);
+        gemm_w4a16_ks2_kernel<BM, BN, WGM, MODE, TILED><<<grid, 512, 0, s>>>(p);
         if (slices > 1) launch_reduce<BM, BN, WGM, MODE>(p, grid, slices, s);
         return;
     }
-    if (p.K % 256 == 0)
-        gemm_w4a16_mfma_kernel<BM, BN, WGM, MODE, true><<<grid, 256, 0, s>>>(p);
-    else
+    if (TILED || p.K % 256 == 0)
+        gemm_w4a16_mfma_kernel<BM, BN, WGM, MODE, true, TILED><<<grid, 256, 0, s>>>(p);
+    else if constexpr (!TILED)
         gemm_w4a16_mfma_kernel<BM, BN, WGM, MODE, false><<<grid, 256, 0, s>>>(p);
     if (slices > 1) launch_reduce<BM, BN, WGM, MODE>(p, grid, slices, s);
 }
@@ -646,7 +659,7 @@ float predict_us(const TileCost& t, int M, int N, int K, int slices, int cus) {
 }
 
 template <int MODE>
-int launch_gemm(GemmParams p, hipStream_t stream, const char* what, float* ws, size_t ws_floats) {
+int launch_gemm(GemmParams p, hipStream_t stream, const char* what, float* ws, size_t ws_floats, bool tiled = false) {
     if (p.M <= 0 || p.N <= 0) return QE_OK;
     p.ws = ws;
     if (ws == nullptr) ws_floats = 0;
@@ -672,11 +685,20 @@ int launch_gemm(GemmParams p, hipStream_t stream, const char* what, float* ws, s
     while (slices > 1 && !fits(kTiles[ti], slices)) --slices;
     const TileCost& t = kTiles[ti];
     if ((p.M + t.bm - 1) / t.bm > 65535) return fail(QE_ERR_UNSUPPORTED, "%s: M=%d too large", what, p.M);
-    switch (ti) {
-        case 0: launch_tiles<64, 64, 2, MODE>(p, slices, stream); break;
-        case 1: launch_tiles<64, 128, 1, MODE>(p, slices, stream); break;
-        case 2: launch_tiles<128, 64, 2, MODE>(p, slices, stream); break;
-        default: launch_tiles<128, 128, 1, MODE>(p, slices, stream); break;
+    if (tiled) {
+        switch (ti) {
+            case 0: launch_tiles<64, 64, 2, MODE, true>(p, slices, stream); break;
+            case 1: launch_tiles<64, 128, 1, MODE, true>(p, slices, stream); break;
+            case 2: launch_tiles<128, 64, 2, MODE, true>(p, slices, stream); break;
+            default: launch_tiles<128, 128, 1, MODE, true>(p, slices, stream); break;
+        }
+    } else {
+        switch (ti) {
+            case 0: launch_tiles<64, 64, 2, MODE>(p, slices, stream); break;
+            case 1: launch_tiles<64, 128, 1, MODE>(p, slices, stream); break;
+            case 2: launch_tiles<128, 64, 2, MODE>(p, slices, stream); break;
+            default: launch_tiles<128, 128, 1, MODE>(p, slices, stream); break;
+        }
     }
     return check_launch(what);
 }
@@ -861,6 +883,34 @@ int launch_gemm_w4a8(GemmParams p, hipStream_t stream, const char* what, float* 
     return check_launch(what);
 }
 
+// Tiled weight layout of the prefill GEMM (K % 256 == 0): the weights of 32
+// columns and one 256-k quad are 4 KB in the order the kernel's lanes load
+// them - load i of lane (h, c) reads 16-byte chunk 8 g + 4 h + i of column c -
+// so each load instruction of a wave reads 1 KB of contiguous memory instead
+// of 64 pieces of different columns.  Columns padded to a multiple of 32
+// (padding is zero).  Scales: for each 32 columns and quad, the 64 fp16
+// scales the lanes need (group 2 g + h of column c at 32 h + c).
+__global__ __launch_bounds__(256) void repack_w4_tiled_kernel(const u32x4* __restrict__ w, const uint16_t* __restrict__ sc,
+                                                           int N, int K, u32x4* __restrict__ wt,
+                                                           uint16_t* __restrict__ st) {
+    const int Q = K >> 8;
+    const int n_pad = (N + 31) & ~31;
+    const size_t chunks = static_cast<size_t>(n_pad) * (K >> 5);
+    const size_t stride = static_cast<size_t>(gridDim.x) * 256;
+    for (size_t t = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; t < chunks; t += stride) {
+        // destination-ordered: t = ((ct * Q + g) * 4 + i) * 64 + 32 h + c
+        const int c = static_cast<int>(t & 31), h = static_cast<int>((t >> 5) & 1), i = static_cast<int>((t >> 6) & 3);
+        const size_t ctg = t >> 8;
+        const int g = static_cast<int>(ctg % Q);
+        const int col = static_cast<int>(ctg / Q) * 32 + c;
+        wt[t] = col < N ? w[static_cast<size_t>(col) * (K >> 5) + 8 * g + 4 * h + i] : u32x4{0u, 0u, 0u, 0u};
+        if (i == 0) {
+            const size_t so = (ctg << 6) + 32 * h + c;
+            st[so] = col < N ? sc[static_cast<size_t>(col) * (K >> 7) + 2 * g + h] : uint16_t(0);
+        }
+    }
+}
+
 // The split-K workspace of `stream` on the current device: allocated by the
 // first launch on that stream that is not being captured into a graph, then
 // kept until the process ends (at most kMaxWsStreams per device; further
@@ -1001,6 +1051,110 @@ extern "C" int qe_launch_gemm_prefill_w4a16_noalloc(const uint32_t* qweight, con
     p.N = N;
     p.K = K;
     return launch_gemm<kPlain>(p, stream, what, ws, kWsFloats);
+}
+
+extern "C" int qe_w4_tiled_bytes(int N, int K, size_t* weight_bytes, size_t* scale_bytes) {
+    QE_REQUIRE(N > 0 && K > 0 && K % 256 == 0, "w4_tiled_bytes: N=%d K=%d (K must be a multiple of 256)", N, K);
+    QE_REQUIRE(weight_bytes && scale_bytes, "w4_tiled_bytes: NULL output");
+    const size_t n_pad = (static_cast<size_t>(N) + 31) & ~size_t(31);
+    *weight_bytes = n_pad * K / 2;
+    *scale_bytes = n_pad * (K / 128) * 2;
+    return QE_OK;
+}
+
+extern "C" int qe_repack_w4_tiled(const uint32_t* qweight, const uint16_t* scales, int N, int K,
+                                  uint32_t* tiled_weight, uint16_t* tiled_scales, hipStream_t stream) {
+    const char* what = "repack_w4_tiled";
+    QE_REQUIRE(qweight && scales && tiled_weight && tiled_scales, "%s: NULL pointer", what);
+    QE_REQUIRE(N > 0 && K > 0 && K % 256 == 0, "%s: N=%d K=%d (K must be a multiple of 256)", what, N, K);
+    QE_REQUIRE(aligned(qweight, 16) && aligned(tiled_weight, 16) && aligned(scales, 2) && aligned(tiled_scales, 2),
+               "%s: weights must be 16-byte aligned", what);
+    const size_t chunks = ((static_cast<size_t>(N) + 31) & ~size_t(31)) * (K >> 5);
+    const unsigned grid = static_cast<unsigned>(std::min<size_t>((chunks + 255) / 256, size_t(cu_count()) * 16));
+    repack_w4_tiled_kernel<<<grid, 256, 0, stream>>>(reinterpret_cast<const u32x4*>(qweight), scales, N, K,
+                                                     reinterpret_cast<u32x4*>(tiled_weight), tiled_scales);
+    return check_launch(what);
+}
+
+extern "C" int qe_launch_gemm_prefill_w4a16_tiled(const uint32_t* tiled_weight, const uint16_t* tiled_scales,
+                                                  const uint16_t* input_x, const uint16_t* residual,
+                                                  uint16_t* output_y, int M, int N, int K, hipStream_t stream) {
+    const char* what = "gemm_prefill_w4a16_tiled";
+    if (int rc = check_gemm_common(what, input_x, M, K)) return rc;
+    QE_REQUIRE(K % 256 == 0, "%s: K=%d must be a multiple of 256", what, K);
+    QE_REQUIRE(tiled_weight && tiled_scales && output_y, "%s: NULL weight/scale/output", what);
+    QE_REQUIRE(N >= 0, "%s: N=%d", what, N);
+    QE_REQUIRE(aligned(tiled_weight, 16) && aligned(tiled_scales, 2), "%s: weights must be 16-byte aligned", what);
+    GemmParams p{};
+    p.qw[0] = tiled_weight;
+    p.sc[0] = tiled_scales;
+    p.out[0] = output_y;
+    p.out_stride[0] = N;
+    p.A = input_x;
+    p.residual = residual;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    return launch_gemm<kPlain>(p, stream, what, gemm_workspace(stream), kWsFloats, true);
+}
+
+extern "C" int qe_launch_gemm_prefill_qkv_w4a16_tiled(const qe_qkv_view* view, const uint16_t* input_x, int M,
+                                                      hipStream_t stream, int in_features, int num_q_heads,
+                                                      int num_kv_heads, int head_dim) {
+    const char* what = "gemm_prefill_qkv_w4a16_tiled";
+    if (int rc = check_gemm_common(what, input_x, M, in_features)) return rc;
+    QE_REQUIRE(in_features % 256 == 0, "%s: in_features=%d must be a multiple of 256", what, in_features);
+    QE_REQUIRE(view != nullptr, "%s: view is NULL", what);
+    QE_REQUIRE(num_q_heads >= 0 && num_kv_heads >= 0 && head_dim >= 0, "%s: negative head shape", what);
+    const int q_dim = num_q_heads * head_dim;
+    const int kv_dim = num_kv_heads * head_dim;
+    // a 32-column tile must not straddle two matrices
+    QE_REQUIRE(q_dim % 32 == 0 && kv_dim % 32 == 0, "%s: q and kv widths must be multiples of 32", what);
+    const void* w[3] = {view->q_weight, view->k_weight, view->v_weight};
+    const uint16_t* s[3] = {view->q_scale, view->k_scale, view->v_scale};
+    uint16_t* o[3] = {view->d_q, view->d_k, view->d_v};
+    const int cols[3] = {q_dim, kv_dim, kv_dim};
+    GemmParams p{};
+    for (int i = 0; i < 3; ++i) {
+        p.out_stride[i] = cols[i];
+        if (cols[i] == 0) continue;
+        QE_REQUIRE(w[i] && s[i] && o[i], "%s: NULL pointer in view (matrix %d)", what, i);
+        QE_REQUIRE(aligned(w[i], 16) && aligned(s[i], 2), "%s: weights must be 16-byte aligned", what);
+        p.qw[i] = static_cast<const uint32_t*>(w[i]);
+        p.sc[i] = s[i];
+        p.out[i] = o[i];
+    }
+    p.col_begin[0] = 0;
+    p.col_begin[1] = q_dim;
+    p.col_begin[2] = q_dim + kv_dim;
+    p.A = input_x;
+    p.M = M;
+    p.N = q_dim + 2 * kv_dim;
+    p.K = in_features;
+    return launch_gemm<kQKV>(p, stream, what, gemm_workspace(stream), kWsFloats, true);
+}
+
+extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled(const uint32_t* tiled_weight,
+                                                                      const uint16_t* tiled_scales,
+                                                                      const uint16_t* input_x, uint16_t* output_mlp,
+                                                                      int M, hipStream_t stream, int hidden_size,
+                                                                      int intermediate_size) {
+    const char* what = "gemm_prefill_dual_gate_up_swiglu_w4a16_tiled";
+    if (int rc = check_gemm_common(what, input_x, M, hidden_size)) return rc;
+    QE_REQUIRE(hidden_size % 256 == 0, "%s: hidden_size=%d must be a multiple of 256", what, hidden_size);
+    QE_REQUIRE(tiled_weight && tiled_scales && output_mlp, "%s: NULL weight/scale/output", what);
+    QE_REQUIRE(intermediate_size >= 0, "%s: intermediate_size=%d", what, intermediate_size);
+    QE_REQUIRE(aligned(tiled_weight, 16) && aligned(tiled_scales, 2), "%s: weights must be 16-byte aligned", what);
+    GemmParams p{};
+    p.qw[0] = tiled_weight;
+    p.sc[0] = tiled_scales;
+    p.out[0] = output_mlp;
+    p.out_stride[0] = intermediate_size;
+    p.A = input_x;
+    p.M = M;
+    p.N = 2 * intermediate_size;
+    p.K = hidden_size;
+    return launch_gemm<kSwiglu>(p, stream, what, gemm_workspace(stream), kWsFloats, true);
 }
 
 extern "C" int qe_launch_gemm_prefill_qkv_w4a16(const qe_qkv_view* view, const uint16_t* input_x, int M,

@@ -33,6 +33,9 @@ SIGNATURES = {
     "qe_launch_gemv_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _I, _I, _P],
     "qe_launch_gemm_prefill_w4a16": [_P, _P, _P, _P, _P, _I, _I, _I, _P, _I],
     "qe_launch_gemm_prefill_w4a16_noalloc": [_P, _P, _P, _P, _P, _I, _I, _I, _P, _I],
+    "qe_launch_gemm_prefill_w4a16_tiled": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "qe_launch_gemm_prefill_qkv_w4a16_tiled": [_P, _P, _I, _P, _I, _I, _I, _I],
+    "qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled": [_P, _P, _P, _P, _I, _P, _I, _I],
     "qe_launch_gemm_prefill_qkv_w4a16": [_P, _P, _I, _P, _I, _I, _I, _I, _I],
     "qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16": [_P, _P, _P, _P, _I, _P, _I, _I],
     "qe_launch_sample_and_advance": [_P, _P, _P, _P, _P, _P, _I],
@@ -59,6 +62,8 @@ OTHER_SIGNATURES = {
     "qe_stream_read": [_P, ctypes.c_size_t, _P, _P],
     "qe_set_tuning": [ctypes.c_char_p, _I],
     "qe_gemm_reserve_workspace": [_P],
+    "qe_w4_tiled_bytes": [_I, _I, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
+    "qe_repack_w4_tiled": [_P, _P, _I, _I, _P, _P, _P],
 }
 
 ENGINE_SIGNATURES = {
@@ -209,6 +214,35 @@ def launch_gemm_prefill_w4a16_noalloc(qweight, scales, input_x, residual, output
                                       sm_count=0):
     _call("qe_launch_gemm_prefill_w4a16_noalloc", _ptr(qweight), _ptr(scales), _ptr(input_x), _ptr(residual),
           _ptr(output_y), M, N, K, _stream(stream), sm_count)
+
+
+def w4_tiled(qweight, scales, N, K, stream=None):
+    """Tiled copy (qe_repack_w4_tiled) of an N x K packed matrix: (weights int32, scales fp16) tensors."""
+    import torch
+    wb, sb = ctypes.c_size_t(), ctypes.c_size_t()
+    _check(lib().qe_w4_tiled_bytes(N, K, ctypes.byref(wb), ctypes.byref(sb)), "qe_w4_tiled_bytes")
+    w = torch.empty(wb.value // 4, dtype=torch.int32, device=qweight.device)
+    s = torch.empty(sb.value // 2, dtype=torch.float16, device=qweight.device)
+    _check(lib().qe_repack_w4_tiled(_ptr(qweight), _ptr(scales), N, K, _ptr(w), _ptr(s), _stream(stream)),
+           "qe_repack_w4_tiled")
+    return w, s
+
+
+def launch_gemm_prefill_w4a16_tiled(tiled_weight, tiled_scales, input_x, residual, output_y, M, N, K, stream=None):
+    _call("qe_launch_gemm_prefill_w4a16_tiled", _ptr(tiled_weight), _ptr(tiled_scales), _ptr(input_x),
+          _ptr(residual), _ptr(output_y), M, N, K, _stream(stream))
+
+
+def launch_gemm_prefill_qkv_w4a16_tiled(view: QKVView, input_x, M, stream=None, in_features=1536, num_q_heads=12,
+                                        num_kv_heads=2, head_dim=128):
+    _call("qe_launch_gemm_prefill_qkv_w4a16_tiled", ctypes.addressof(view), _ptr(input_x), M, _stream(stream),
+          in_features, num_q_heads, num_kv_heads, head_dim)
+
+
+def launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled(tiled_weight, tiled_scales, input_x, output_mlp, M,
+                                                        stream=None, hidden_size=1536, intermediate_size=8960):
+    _call("qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled", _ptr(tiled_weight), _ptr(tiled_scales),
+          _ptr(input_x), _ptr(output_mlp), M, _stream(stream), hidden_size, intermediate_size)
 
 
 def launch_gemm_prefill_qkv_w4a16(view: QKVView, input_x, M, stream=None, in_features=1536, num_q_heads=12,

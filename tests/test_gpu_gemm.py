@@ -324,3 +324,59 @@ def test_gemm_captured_without_workspace_matches_tolerance(qe, orc):
             outs.append(host(out).copy())
         assert all(np.array_equal(o.view(np.uint16), outs[0].view(np.uint16)) for o in outs)
         assert_fp16_close(outs[0][:16], ex, bd, ref, what=f"captured gemm reserve={reserve}")
+
+
+# ---- tiled weight layout (load-time repack) ----------------------------------------
+@pytest.mark.parametrize("M,N,K", [(128, 1536, 1536), (128, 17920, 1536), (64, 1536, 8960), (1024, 1536, 1536),
+                                   (37, 1000, 768), (300, 130, 256), (1, 33, 512)])
+def test_gemm_tiled_layout_bit_identical(qe, orc, M, N, K):
+    """The GEMM on the tiled copy gives the bits of the GEMM on the .qwenbin
+    layout (same plan, same arithmetic), with and without a residual, and
+    matches the oracle."""
+    print(f"gemm tiled M={M} N={N} K={K}", flush=True)
+    qw, sc = orc.synth_w4(M + 5 * N + K, N, K)
+    A = _A(orc, M, K, 61)
+    R = orc.synth_f16_normal(62, M * N).reshape(M, N)
+    dq, ds = dev(qw), dev(sc)
+    tw, ts = qe.w4_tiled(dq, ds, N, K)
+    pad = (N + 31) // 32 * 32
+    assert tw.numel() == pad * K // 8 and ts.numel() == pad * K // 128
+    for res in (None, R):
+        a, b = empty((M, N), torch.float16), empty((M, N), torch.float16)
+        dres = dev(res) if res is not None else None
+        qe.launch_gemm_prefill_w4a16(dq, ds, dev(A), dres, a, M, N, K)
+        qe.launch_gemm_prefill_w4a16_tiled(tw, ts, dev(A), dres, b, M, N, K)
+        assert np.array_equal(host(a).view(np.uint16), host(b).view(np.uint16))
+    rows = min(M, 16)
+    ref, ex, bd = orc.gemm_w4a16(qw, sc, A[:rows], rows, N, K)
+    qe.launch_gemm_prefill_w4a16_tiled(tw, ts, dev(A), None, b, M, N, K)
+    assert_fp16_close(host(b)[:rows], ex, bd, ref, what="tiled gemm")
+
+
+def test_gemm_tiled_qkv_and_swiglu_bit_identical(qe, orc):
+    M, H, I = 160, 1536, 4096
+    A = _A(orc, M, H, 63)
+    for nq, nkv, hd in ((12, 2, 128), (4, 1, 64), (3, 3, 96)):
+        dims = (nq * hd, nkv * hd, nkv * hd)
+        mats = [orc.synth_w4(70 + i + nq, n, H) for i, n in enumerate(dims)]
+        dw = [(dev(w), dev(s)) for w, s in mats]
+        tw = [qe.w4_tiled(w, s, n, H) for (w, s), n in zip(dw, dims)]
+        outs = [[empty((M, n), torch.float16) for n in dims] for _ in range(2)]
+        v0 = qe.make_qkv_view(dw[0][0], dw[0][1], outs[0][0], dw[1][0], dw[1][1], outs[0][1], dw[2][0], dw[2][1],
+                              outs[0][2])
+        v1 = qe.make_qkv_view(tw[0][0], tw[0][1], outs[1][0], tw[1][0], tw[1][1], outs[1][1], tw[2][0], tw[2][1],
+                              outs[1][2])
+        qe.launch_gemm_prefill_qkv_w4a16(v0, dev(A), M, in_features=H, num_q_heads=nq, num_kv_heads=nkv, head_dim=hd)
+        qe.launch_gemm_prefill_qkv_w4a16_tiled(v1, dev(A), M, in_features=H, num_q_heads=nq, num_kv_heads=nkv,
+                                               head_dim=hd)
+        for a, b in zip(outs[0], outs[1]):
+            assert np.array_equal(host(a).view(np.uint16), host(b).view(np.uint16)), (nq, nkv, hd)
+    qgu, sgu = orc.synth_w4(80, 2 * I, H)
+    dq, ds = dev(qgu), dev(sgu)
+    tw, ts = qe.w4_tiled(dq, ds, 2 * I, H)
+    a, b = empty((M, I), torch.float16), empty((M, I), torch.float16)
+    qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a16(dq, ds, dev(A), a, M, hidden_size=H, intermediate_size=I)
+    qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled(tw, ts, dev(A), b, M, hidden_size=H, intermediate_size=I)
+    assert np.array_equal(host(a).view(np.uint16), host(b).view(np.uint16))
+    with pytest.raises(RuntimeError, match="multiple of 256"):
+        qe.launch_gemm_prefill_w4a16_tiled(tw, ts, dev(A), None, b, M, 64, 128)
