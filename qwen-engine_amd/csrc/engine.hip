@@ -69,6 +69,7 @@ struct Mat {
 struct Layer {
     uint16_t *ln1, *ln2, *q_bias, *k_bias, *v_bias;
     Mat q, k, v, o, gate_up, down;
+    Mat tq, tk, tv, to, tgate_up, tdown;  // tiled copies for the prefill GEMMs (qe_repack_w4_tiled)
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -101,6 +102,7 @@ struct qe_engine {
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     int seq_pos = 0;
+    bool tiled = false;  // prefill GEMMs read the tiled copies
 
     template <class T>
     T* take(size_t bytes) {
@@ -266,21 +268,35 @@ int prefill_chunk(qe_engine* e, int start, int len) {
         uint16_t* kc = e->kcache + l * e->kv_stride();
         uint16_t* vc = e->vcache + l * e->kv_stride();
         QE_TRY(qe_launch_rmsnorm_fp16(e->act0, L.ln1, e->act1, len, s, H));
-        const qe_qkv_view view = view_of(e, L, e->dq, e->dk, e->dv);
-        QE_TRY(qe_launch_gemm_prefill_qkv_w4a16(&view, e->act1, len, s, H, c.num_q_heads, c.num_kv_heads,
-                                                c.head_dim, 0));
+        if (e->tiled) {
+            const qe_qkv_view tv{L.tq.w, L.tq.s, e->dq, L.tk.w, L.tk.s, e->dk, L.tv.w, L.tv.s, e->dv};
+            QE_TRY(qe_launch_gemm_prefill_qkv_w4a16_tiled(&tv, e->act1, len, s, H, c.num_q_heads, c.num_kv_heads,
+                                                          c.head_dim));
+        } else {
+            const qe_qkv_view view = view_of(e, L, e->dq, e->dk, e->dv);
+            QE_TRY(qe_launch_gemm_prefill_qkv_w4a16(&view, e->act1, len, s, H, c.num_q_heads, c.num_kv_heads,
+                                                    c.head_dim, 0));
+        }
         QE_TRY(qe_launch_qkv_bias_rope_kv_append(e->dq, e->dk, e->dv, L.q_bias, L.k_bias, L.v_bias, kc, vc, e->ctl,
                                                  len, s, c.num_q_heads, c.num_kv_heads, c.head_dim, c.max_seq_len,
                                                  c.head_dim, c.rope_theta));
         QE_TRY(qe_launch_attention_gqa_prefill(e->dq, kc, vc, e->attn, e->ctl, len, s, c.num_q_heads,
                                                c.num_kv_heads, c.head_dim, c.max_seq_len,
                                                c.num_q_heads * c.head_dim));
-        QE_TRY(qe_launch_gemm_prefill_w4a16(L.o.w, L.o.s, e->attn, e->act0, e->act0, len, H,
-                                            c.num_q_heads * c.head_dim, s, 0));
-        QE_TRY(qe_launch_rmsnorm_fp16(e->act0, L.ln2, e->act1, len, s, H));
-        QE_TRY(qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(L.gate_up.w, L.gate_up.s, e->act1, e->mlp, len, s, H,
-                                                                I));
-        QE_TRY(qe_launch_gemm_prefill_w4a16(L.down.w, L.down.s, e->mlp, e->act0, e->act0, len, H, I, s, 0));
+        const int qd = c.num_q_heads * c.head_dim;
+        if (e->tiled) {
+            QE_TRY(qe_launch_gemm_prefill_w4a16_tiled(L.to.w, L.to.s, e->attn, e->act0, e->act0, len, H, qd, s));
+            QE_TRY(qe_launch_rmsnorm_fp16(e->act0, L.ln2, e->act1, len, s, H));
+            QE_TRY(qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled(L.tgate_up.w, L.tgate_up.s, e->act1, e->mlp,
+                                                                          len, s, H, I));
+            QE_TRY(qe_launch_gemm_prefill_w4a16_tiled(L.tdown.w, L.tdown.s, e->mlp, e->act0, e->act0, len, H, I, s));
+        } else {
+            QE_TRY(qe_launch_gemm_prefill_w4a16(L.o.w, L.o.s, e->attn, e->act0, e->act0, len, H, qd, s, 0));
+            QE_TRY(qe_launch_rmsnorm_fp16(e->act0, L.ln2, e->act1, len, s, H));
+            QE_TRY(qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(L.gate_up.w, L.gate_up.s, e->act1, e->mlp, len,
+                                                                    s, H, I));
+            QE_TRY(qe_launch_gemm_prefill_w4a16(L.down.w, L.down.s, e->mlp, e->act0, e->act0, len, H, I, s, 0));
+        }
     }
     return QE_OK;
 }
@@ -348,6 +364,55 @@ size_t weight_bytes(const qe_engine_config& c) {
     return per_layer * c.num_layers + mat_bytes(c.vocab_size, H) + align256(H * 2);
 }
 
+// Tiled copies of the layer matrices for the prefill GEMMs: every K a
+// multiple of 256 and the QKV widths multiples of 32 (0 bytes otherwise, or
+// when switched off with qe_set_tuning("engine_tiled_prefill", 0)).
+size_t tiled_mat_bytes(int rows, int K) {
+    size_t w = 0, sb = 0;
+    if (qe_w4_tiled_bytes(rows, K, &w, &sb) != QE_OK) return 0;
+    return align256(w) + align256(sb);
+}
+
+bool tiled_ok(const qe_engine_config& c) {
+    const int qd = c.num_q_heads * c.head_dim, kvd = c.num_kv_heads * c.head_dim;
+    return engine_tiled_prefill() && c.hidden_size % 256 == 0 && c.intermediate_size % 256 == 0 && qd % 256 == 0 &&
+           qd % 32 == 0 && kvd % 32 == 0;
+}
+
+size_t tiled_bytes(const qe_engine_config& c) {
+    if (!tiled_ok(c)) return 0;
+    const int H = c.hidden_size, I = c.intermediate_size, qd = c.num_q_heads * c.head_dim,
+              kvd = c.num_kv_heads * c.head_dim;
+    return static_cast<size_t>(c.num_layers) *
+           (tiled_mat_bytes(qd, H) + 2 * tiled_mat_bytes(kvd, H) + tiled_mat_bytes(H, qd) +
+            tiled_mat_bytes(2 * I, H) + tiled_mat_bytes(H, I));
+}
+
+// Carves the tiled copies out of the arena and writes them (on the engine's
+// stream, after the weights are in place).
+int setup_tiled(qe_engine* e) {
+    if (!tiled_ok(e->cfg)) return QE_OK;
+    auto tile = [&](const Mat& m, Mat& t) -> int {
+        size_t wb = 0, sb = 0;
+        QE_TRY(qe_w4_tiled_bytes(m.rows, m.K, &wb, &sb));
+        t.rows = m.rows;
+        t.K = m.K;
+        t.w = e->take<uint32_t>(wb);
+        t.s = e->take<uint16_t>(sb);
+        return qe_repack_w4_tiled(m.w, m.s, m.rows, m.K, t.w, t.s, e->stream);
+    };
+    for (Layer& L : e->layers) {
+        QE_TRY(tile(L.q, L.tq));
+        QE_TRY(tile(L.k, L.tk));
+        QE_TRY(tile(L.v, L.tv));
+        QE_TRY(tile(L.o, L.to));
+        QE_TRY(tile(L.gate_up, L.tgate_up));
+        QE_TRY(tile(L.down, L.tdown));
+    }
+    e->tiled = true;
+    return QE_OK;
+}
+
 // Q8_1 scratch holds the longest quantized activation: the down input (I),
 // the normalized hidden state (H) or the attention output (q_dim)
 int q8_len(const qe_engine_config& c) {
@@ -365,7 +430,7 @@ size_t workspace_bytes(const qe_engine_config& c) {
     bytes += 2 * align256(static_cast<size_t>(c.num_q_heads) * 16 * 128 * 4) +
              2 * align256(QE_LM_HEAD_SAMPLE_PARTS * 4) + align256(static_cast<size_t>(c.max_seq_len) * 4) + 256 +
              256 + 4096;
-    return bytes;
+    return bytes + tiled_bytes(c);
 }
 
 int begin_engine(qe_engine* e, const qe_engine_config& c, size_t arena_bytes) {
@@ -406,6 +471,7 @@ void layout_workspace(qe_engine* e) {
 
 // KV cache cleared, control block at position 0, decode graph captured
 int finish_engine(qe_engine* e) {
+    QE_TRY(setup_tiled(e));
     QE_REQUIRE(e->arena_used <= e->arena_size, "engine_create: arena overflow (%zu > %zu)", e->arena_used,
                e->arena_size);
     (void)cu_count();  // cache the device fact before graph capture

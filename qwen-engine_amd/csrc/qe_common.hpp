@@ -29,6 +29,7 @@ int gemm_forced_slices();  // 0 auto, else K slices
 int gemm_ks2_mode();       // 0 auto, 1 never, 2 always (K % 256 == 0): the two-group k split
 int gemv_forced_bt();      // 0 auto, else GEMV block size (256, 512, 1024)
 int gemv_forced_cap();     // 0 auto, else the largest GEMV grid (larger grids loop over row sets)
+int engine_tiled_prefill();  // engines created from now on keep tiled copies for the prefill GEMMs (default 1)
 
 inline int fail(int code, const char* fmt, ...) {
     char buf[512];

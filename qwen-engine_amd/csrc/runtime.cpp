@@ -20,6 +20,7 @@ int g_gemm_slices = 0;
 int g_gemm_ks2 = 0;
 int g_gemv_bt = 0;
 int g_gemv_cap = 0;
+int g_engine_tiled = 1;
 }  // namespace
 
 int gemm_split_k_enabled() { return g_gemm_split_k; }
@@ -28,6 +29,7 @@ int gemm_forced_slices() { return g_gemm_slices; }
 int gemm_ks2_mode() { return g_gemm_ks2; }
 int gemv_forced_bt() { return g_gemv_bt; }
 int gemv_forced_cap() { return g_gemv_cap; }
+int engine_tiled_prefill() { return g_engine_tiled; }
 
 void set_error(const char* fmt, ...) {
     va_list ap;
@@ -81,6 +83,10 @@ extern "C" int qe_set_tuning(const char* key, int value) {
     if (std::strcmp(key, "gemm_ks2") == 0) {
         if (value < 0 || value > 2) return qe::fail(QE_ERR_INVALID_ARGUMENT, "set_tuning: gemm_ks2 %d not in 0..2", value);
         qe::g_gemm_ks2 = value;
+        return QE_OK;
+    }
+    if (std::strcmp(key, "engine_tiled_prefill") == 0) {
+        qe::g_engine_tiled = value != 0;
         return QE_OK;
     }
     if (std::strcmp(key, "gemm_slices") == 0) {

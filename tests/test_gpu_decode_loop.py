@@ -298,3 +298,25 @@ def test_engine_prefill_lm_head_matches_oracle(qe, orc):
     assert engines[0][1] == engines[1][1]
     for e, _ in engines:
         e.close()
+
+
+def test_engine_tiled_prefill_matches_qwenbin_layout(qe):
+    """The engine's prefill on the tiled weight copies gives the same hidden
+    rows, logits and tokens as on the .qwenbin layout, over a multi-chunk
+    prompt (chunk 64)."""
+    prompt = [(i % 1000) + 100 for i in range(150)]
+    outs = []
+    for tiled in (1, 0):
+        qe.set_tuning("engine_tiled_prefill", tiled)
+        try:
+            e = qe.Engine(_small_cfg(qe), seed=11)
+        finally:
+            qe.set_tuning("engine_tiled_prefill", 1)
+        t = e.prefill(prompt)
+        hid = e.read("hidden", np.float16, 64 * 1536)
+        outs.append((t, hid.view(np.uint16).copy(), e.logits().view(np.uint16).copy(), e.decode(4)))
+        e.close()
+    assert outs[0][0] == outs[1][0]
+    assert np.array_equal(outs[0][1], outs[1][1])
+    assert np.array_equal(outs[0][2], outs[1][2])
+    assert outs[0][3] == outs[1][3]
