@@ -14,6 +14,7 @@
 
 #include <cerrno>
 #include <cstdio>
+#include <cmath>
 #include <cstring>
 
 #include "qe_common.hpp"
@@ -92,6 +93,10 @@ int qwenbin_parse(const MappedFile& file, QwenbinModel& m) {
                     static_cast<unsigned long long>(I), static_cast<unsigned long long>(NQ),
                     static_cast<unsigned long long>(NKV), static_cast<unsigned long long>(HD),
                     static_cast<unsigned long long>(V), static_cast<unsigned long long>(L));
+    // the RMSNorm kernels use eps = 1e-6 (RMS_NORM_EPS, include/config.cuh:20), as the reference's do
+    if (!(std::fabs(h.rms_norm_eps - 1e-6f) <= 1e-12f))
+        return fail(QE_ERR_UNSUPPORTED, "qwenbin: rms_norm_eps %g is not supported (the kernels use 1e-6)",
+                    static_cast<double>(h.rms_norm_eps));
     if (h.layer_table_offset < sizeof(qe_qwenbin_header) || h.layer_table_offset > size ||
         L * sizeof(qe_qwenbin_layer) > size - h.layer_table_offset)
         return fail(QE_ERR_INVALID_ARGUMENT, "qwenbin: truncated layer table (offset %llu, %llu layers, file %llu)",

@@ -57,6 +57,7 @@ def _expect_fail(qe, path, code, text):
     ("misaligned_q", "not 16-byte aligned"),
     ("no_embed_scales", "embed_tokens"),
     ("head_dim", "dimensions outside"),
+    ("eps", "rms_norm_eps"),
 ])
 def test_malformed_containers_rejected(qe, tmp_path, case, text):
     m = qw.synth_model(L=2, seed=3)
@@ -85,6 +86,8 @@ def test_malformed_containers_rejected(qe, tmp_path, case, text):
             h[21] = 0
         elif case == "head_dim":
             h[7] = 64
+        elif case == "eps":
+            h[12] = 1e-5
 
     qw.write(p, m, mutate=mutate)
     _expect_fail(qe, p, None, text)
