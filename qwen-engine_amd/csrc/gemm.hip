@@ -136,6 +136,52 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, const f32x16 (&acc
             epilogue_frag<MODE>(p, acc[i][j], m0 + wm * WM + i * 32, n0 + wn * WN + j * 32 + (lane & 31), lane);
 }
 
+// Nibble order of a word of the tiled copy: k0 at bits 0-3, k1 at 16-19, k2 at
+// 4-7, k3 at 20-23, k4 at 8-11, k5 at 24-27, k6 at 12-15, k7 at 28-31.  A
+// nibble in bits 0-3 of a 16-bit half under the exponent of 1024.0 (0x6400)
+// reads as 1024 + q; in bits 4-7 under the exponent of 64.0 (0x5400) as
+// 64 + q.  So the 8 values in K order cost five bit operations (two masked
+// ORs, a shift, two masked ORs), then the exact subtraction of 1032 or 72 and
+// the one fp16 RNE multiply by the scale of unpack_w4_to_half8 - the same
+// values as unpack_w4_to_half8 on the original word.
+// The four masks live in VGPRs (TiledMasks, set up once per kernel): gfx9
+// VOP3 instructions take no literal constants, so with literal masks the
+// compiler emits separate AND and OR instructions instead of V_AND_OR_B32.
+struct TiledMasks {
+    uint32_t lo, hi, bias_lo, bias_hi;
+};
+__device__ __forceinline__ TiledMasks tiled_masks() {
+    TiledMasks m{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x54005400u};
+    asm volatile("" : "+v"(m.lo), "+v"(m.hi), "+v"(m.bias_lo), "+v"(m.bias_hi));
+    return m;
+}
+__device__ __forceinline__ qwen::qe_half8_t unpack_w4t_to_half8(uint32_t w, _Float16 scale, const TiledMasks& m) {
+    const uint32_t w8 = w >> 8;
+    const uint32_t u01 = (w & m.lo) | m.bias_lo;
+    const uint32_t u23 = (w & m.hi) | m.bias_hi;
+    const uint32_t u45 = (w8 & m.lo) | m.bias_lo;
+    const uint32_t u67 = (w8 & m.hi) | m.bias_hi;
+    const qwen::qe_half2_t b1 = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const qwen::qe_half2_t b2 = {(_Float16)72.0f, (_Float16)72.0f};
+    const qwen::qe_half2_t sc = {scale, scale};
+    const qwen::qe_half2_t h01 = (__builtin_bit_cast(qwen::qe_half2_t, u01) - b1) * sc;
+    const qwen::qe_half2_t h23 = (__builtin_bit_cast(qwen::qe_half2_t, u23) - b2) * sc;
+    const qwen::qe_half2_t h45 = (__builtin_bit_cast(qwen::qe_half2_t, u45) - b1) * sc;
+    const qwen::qe_half2_t h67 = (__builtin_bit_cast(qwen::qe_half2_t, u67) - b2) * sc;
+    return qwen::qe_half8_t{h01[0], h01[1], h23[0], h23[1], h45[0], h45[1], h67[0], h67[1]};
+}
+
+// The same 8 values of an original word, in the tiled word's nibble order.
+__device__ __forceinline__ uint32_t w4_word_to_tiled(uint32_t w) {
+    uint32_t q[8];
+    q[0] = w & 15u;          q[4] = (w >> 4) & 15u;
+    q[1] = (w >> 8) & 15u;   q[5] = (w >> 12) & 15u;
+    q[2] = (w >> 16) & 15u;  q[6] = (w >> 20) & 15u;
+    q[3] = (w >> 24) & 15u;  q[7] = (w >> 28) & 15u;
+    return q[0] | (q[2] << 4) | (q[4] << 8) | (q[6] << 12) | (q[1] << 16) | (q[3] << 20) | (q[5] << 24) |
+           (q[7] << 28);
+}
+
 // Block tile BM x BN, 4 waves in a WGM x (4/WGM) grid, wave tile WM x WN of
 // 32x32 MFMA tiles.  K advances 64 per step.  grid (N tiles, M tiles, K
 // slices); with more than one slice the fp32 partials go to the scratch.
@@ -183,6 +229,7 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
     const int KT = kt_end - kt_begin;
     const int fr = lane & 31;
     const int h = lane >> 5;
+    const TiledMasks tmask = tiled_masks();
 
     // A: rows past M read row M-1 (valid) and are never stored
     const int a_row = tid >> 3;
@@ -282,7 +329,8 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a16_mfma_kernel(GemmParams p) {
 #pragma unroll
             for (int j = 0; j < NI; ++j) {
                 const uint32_t w = QUAD ? rb[e][j][t][s] : rb[e][j][0][s];
-                bf[j] = __builtin_bit_cast(f16x8, qwen::unpack_w4_to_half8(w, __builtin_bit_cast(_Float16, rs[e][j])));
+                const _Float16 sc = __builtin_bit_cast(_Float16, rs[e][j]);
+                bf[j] = __builtin_bit_cast(f16x8, TILED ? unpack_w4t_to_half8(w, sc, tmask) : qwen::unpack_w4_to_half8(w, sc));
             }
         };
         // software pipeline over the four sub-steps: the A fragments and the
@@ -393,6 +441,7 @@ __global__ __launch_bounds__(512, 1) void gemm_w4a16_ks2_kernel(GemmParams p) {
     const int KTL = (kt_end - kt_begin) / 2;  // steps per group
     const int fr = lane & 31;
     const int h = lane >> 5;
+    const TiledMasks tmask = tiled_masks();
 
     const int a_row = gtid >> 3;
     const int c = gtid & 7;
@@ -457,8 +506,10 @@ __global__ __launch_bounds__(512, 1) void gemm_w4a16_ks2_kernel(GemmParams p) {
     auto dequant = [&](int e, int tt, int s, f16x8 (&bf)[NI]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < NI; ++j)
-            bf[j] = __builtin_bit_cast(f16x8, qwen::unpack_w4_to_half8(rb[e][j][tt][s],
-                                                                        __builtin_bit_cast(_Float16, rs[e][j])));
+            bf[j] = __builtin_bit_cast(f16x8, TILED ? unpack_w4t_to_half8(rb[e][j][tt][s],
+                                                                          __builtin_bit_cast(_Float16, rs[e][j]), tmask)
+                                                    : qwen::unpack_w4_to_half8(rb[e][j][tt][s],
+                                                                               __builtin_bit_cast(_Float16, rs[e][j])));
     };
 
     f32x16 acc[MI][NI];
@@ -887,8 +938,9 @@ int launch_gemm_w4a8(GemmParams p, hipStream_t stream, const char* what, float* 
 // columns and one 256-k quad are 4 KB in the order the kernel's lanes load
 // them - load i of lane (h, c) reads 16-byte chunk 8 g + 4 h + i of column c -
 // so each load instruction of a wave reads 1 KB of contiguous memory instead
-// of 64 pieces of different columns.  Columns padded to a multiple of 32
-// (padding is zero).  Scales: for each 32 columns and quad, the 64 fp16
+// of 64 pieces of different columns, and each word holds its 8 nibbles in the
+// order unpack_w4t_to_half8 reads fastest.  Columns padded to a multiple of
+// 32 (weights q = 8, scales 0: the padding is zero).  Scales: for each 32 columns and quad, the 64 fp16
 // scales the lanes need (group 2 g + h of column c at 32 h + c).
 __global__ __launch_bounds__(256) void repack_w4_tiled_kernel(const u32x4* __restrict__ w, const uint16_t* __restrict__ sc,
                                                            int N, int K, u32x4* __restrict__ wt,
@@ -903,7 +955,12 @@ __global__ __launch_bounds__(256) void repack_w4_tiled_kernel(const u32x4* __res
         const size_t ctg = t >> 8;
         const int g = static_cast<int>(ctg % Q);
         const int col = static_cast<int>(ctg / Q) * 32 + c;
-        wt[t] = col < N ? w[static_cast<size_t>(col) * (K >> 5) + 8 * g + 4 * h + i] : u32x4{0u, 0u, 0u, 0u};
+        u32x4 v = u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};  // padding: q = 8, i.e. 0
+        if (col < N) {
+            v = w[static_cast<size_t>(col) * (K >> 5) + 8 * g + 4 * h + i];
+            v = u32x4{w4_word_to_tiled(v.x), w4_word_to_tiled(v.y), w4_word_to_tiled(v.z), w4_word_to_tiled(v.w)};
+        }
+        wt[t] = v;
         if (i == 0) {
             const size_t so = (ctg << 6) + 32 * h + c;
             st[so] = col < N ? sc[static_cast<size_t>(col) * (K >> 7) + 2 * g + h] : uint16_t(0);
