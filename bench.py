@@ -124,11 +124,16 @@ def main():
         qw, sc = rand_w4(2 * I, H, 1)
         A = torch.randn((M, H), device=dev, generator=gen).half()
         outp = torch.empty((M, I), dtype=torch.float16, device=dev)
+        tw, ts = qe_amd.w4_tiled(qw[0], sc[0], 2 * I, H)
         for _ in range(20):
             qe_amd.launch_gemm_prefill_dual_gate_up_swiglu_w4a16(qw[0], sc[0], A, outp, M, hidden_size=H,
                                                                  intermediate_size=I)
+        for _ in range(20):
+            qe_amd.launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled(tw, ts, A, outp, M, hidden_size=H,
+                                                                       intermediate_size=I)
         torch.cuda.synchronize()
-        print(json.dumps({"only_prefill_gemm": {"M": M, "N": 2 * I, "K": H, "launches": 20}}))
+        print(json.dumps({"only_prefill_gemm": {"M": M, "N": 2 * I, "K": H, "launches": "20 .qwenbin layout, "
+                                                                                         "then 20 tiled"}}))
         return
     if args.only_decode:
         eng = qe_amd.Engine(qe_amd.default_config(), seed=2024)
