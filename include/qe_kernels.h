@@ -188,9 +188,11 @@ int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_qwe
  * 32 columns and 256-k quad g, 4 KB of weights as [i 0..3][h 0..1][c 0..31]
  * 16-byte chunks (chunk 8g + 4h + i of column c), and 64 fp16 scales as
  * [h][c] (group 2g + h of column c).  Columns are padded to a multiple of 32
- * (zeros).  Requires K % 256 == 0.  Same tile and K-slice plan, and the same
- * bits, as the .qwenbin-layout launchers; 5-13 % faster on MI355X at the
- * Qwen2.5-1.5B shapes (fewer cache lines per load instruction). */
+ * (zeros), and each word holds its nibbles in the order the dequantization
+ * reads fastest.  Requires K % 256 == 0.  For a given tile and K-slice plan
+ * the results equal the .qwenbin-layout launchers' bit for bit; the plan
+ * comes from a time model fitted to these kernels.  10-20 % faster on
+ * MI355X at the Qwen2.5-1.5B shapes. */
 
 /* Bytes of the tiled copy of an N x K matrix (weights, scales). */
 int qe_w4_tiled_bytes(int N, int K, size_t* weight_bytes, size_t* scale_bytes);

@@ -302,8 +302,8 @@ def test_engine_prefill_lm_head_matches_oracle(qe, orc):
 
 def test_engine_tiled_prefill_matches_qwenbin_layout(qe):
     """The engine's prefill on the tiled weight copies gives the same hidden
-    rows, logits and tokens as on the .qwenbin layout, over a multi-chunk
-    prompt (chunk 64)."""
+    rows, logits and tokens as on the .qwenbin layout for the same GEMM plan,
+    over a multi-chunk prompt (chunk 64)."""
     prompt = [(i % 1000) + 100 for i in range(150)]
     outs = []
     for tiled in (1, 0):
@@ -312,7 +312,13 @@ def test_engine_tiled_prefill_matches_qwenbin_layout(qe):
             e = qe.Engine(_small_cfg(qe), seed=11)
         finally:
             qe.set_tuning("engine_tiled_prefill", 1)
-        t = e.prefill(prompt)
+        qe.set_tuning("gemm_tile", 2)
+        qe.set_tuning("gemm_slices", 2)
+        try:
+            t = e.prefill(prompt)
+        finally:
+            qe.set_tuning("gemm_tile", 0)
+            qe.set_tuning("gemm_slices", 0)
         hid = e.read("hidden", np.float16, 64 * 1536)
         outs.append((t, hid.view(np.uint16).copy(), e.logits().view(np.uint16).copy(), e.decode(4)))
         e.close()

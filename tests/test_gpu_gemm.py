@@ -331,8 +331,8 @@ def test_gemm_captured_without_workspace_matches_tolerance(qe, orc):
                                    (37, 1000, 768), (300, 130, 256), (1, 33, 512)])
 def test_gemm_tiled_layout_bit_identical(qe, orc, M, N, K):
     """The GEMM on the tiled copy gives the bits of the GEMM on the .qwenbin
-    layout (same plan, same arithmetic), with and without a residual, and
-    matches the oracle."""
+    layout for the same tile and K-slice plan (the same arithmetic), with and
+    without a residual, and matches the oracle with its own plan."""
     print(f"gemm tiled M={M} N={N} K={K}", flush=True)
     qw, sc = orc.synth_w4(M + 5 * N + K, N, K)
     A = _A(orc, M, K, 61)
@@ -341,16 +341,31 @@ def test_gemm_tiled_layout_bit_identical(qe, orc, M, N, K):
     tw, ts = qe.w4_tiled(dq, ds, N, K)
     pad = (N + 31) // 32 * 32
     assert tw.numel() == pad * K // 8 and ts.numel() == pad * K // 128
-    for res in (None, R):
+    for res, plan in ((None, (4, 1)), (R, (2, 2)), (None, (1, 3))):
         a, b = empty((M, N), torch.float16), empty((M, N), torch.float16)
         dres = dev(res) if res is not None else None
-        qe.launch_gemm_prefill_w4a16(dq, ds, dev(A), dres, a, M, N, K)
-        qe.launch_gemm_prefill_w4a16_tiled(tw, ts, dev(A), dres, b, M, N, K)
-        assert np.array_equal(host(a).view(np.uint16), host(b).view(np.uint16))
+        with forced_plan(qe, *plan):
+            qe.launch_gemm_prefill_w4a16(dq, ds, dev(A), dres, a, M, N, K)
+            qe.launch_gemm_prefill_w4a16_tiled(tw, ts, dev(A), dres, b, M, N, K)
+        assert np.array_equal(host(a).view(np.uint16), host(b).view(np.uint16)), plan
     rows = min(M, 16)
     ref, ex, bd = orc.gemm_w4a16(qw, sc, A[:rows], rows, N, K)
     qe.launch_gemm_prefill_w4a16_tiled(tw, ts, dev(A), None, b, M, N, K)
     assert_fp16_close(host(b)[:rows], ex, bd, ref, what="tiled gemm")
+
+
+class forced_plan:
+    """Forces the prefill GEMM tile (1..4) and K-slice count while active."""
+    def __init__(self, qe, tile, slices):
+        self.qe, self.tile, self.slices = qe, tile, slices
+
+    def __enter__(self):
+        self.qe.set_tuning("gemm_tile", self.tile)
+        self.qe.set_tuning("gemm_slices", self.slices)
+
+    def __exit__(self, *exc):
+        self.qe.set_tuning("gemm_tile", 0)
+        self.qe.set_tuning("gemm_slices", 0)
 
 
 def test_gemm_tiled_qkv_and_swiglu_bit_identical(qe, orc):
@@ -366,17 +381,24 @@ def test_gemm_tiled_qkv_and_swiglu_bit_identical(qe, orc):
                               outs[0][2])
         v1 = qe.make_qkv_view(tw[0][0], tw[0][1], outs[1][0], tw[1][0], tw[1][1], outs[1][1], tw[2][0], tw[2][1],
                               outs[1][2])
-        qe.launch_gemm_prefill_qkv_w4a16(v0, dev(A), M, in_features=H, num_q_heads=nq, num_kv_heads=nkv, head_dim=hd)
-        qe.launch_gemm_prefill_qkv_w4a16_tiled(v1, dev(A), M, in_features=H, num_q_heads=nq, num_kv_heads=nkv,
-                                               head_dim=hd)
+        with forced_plan(qe, 2, 2):
+            qe.launch_gemm_prefill_qkv_w4a16(v0, dev(A), M, in_features=H, num_q_heads=nq, num_kv_heads=nkv,
+                                             head_dim=hd)
+            qe.launch_gemm_prefill_qkv_w4a16_tiled(v1, dev(A), M, in_features=H, num_q_heads=nq, num_kv_heads=nkv,
+                                                   head_dim=hd)
         for a, b in zip(outs[0], outs[1]):
             assert np.array_equal(host(a).view(np.uint16), host(b).view(np.uint16)), (nq, nkv, hd)
     qgu, sgu = orc.synth_w4(80, 2 * I, H)
     dq, ds = dev(qgu), dev(sgu)
     tw, ts = qe.w4_tiled(dq, ds, 2 * I, H)
     a, b = empty((M, I), torch.float16), empty((M, I), torch.float16)
-    qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a16(dq, ds, dev(A), a, M, hidden_size=H, intermediate_size=I)
-    qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled(tw, ts, dev(A), b, M, hidden_size=H, intermediate_size=I)
+    with forced_plan(qe, 4, 1):
+        qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a16(dq, ds, dev(A), a, M, hidden_size=H, intermediate_size=I)
+        qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled(tw, ts, dev(A), b, M, hidden_size=H,
+                                                               intermediate_size=I)
     assert np.array_equal(host(a).view(np.uint16), host(b).view(np.uint16))
+    ref, ex, bd = orc.gemm_swiglu_w4a16(qgu, sgu, A[:8], 8, H, I)
+    qe.launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled(tw, ts, dev(A), b, M, hidden_size=H, intermediate_size=I)
+    assert_fp16_close(host(b)[:8], ex, bd, ref, what="tiled swiglu, own plan")
     with pytest.raises(RuntimeError, match="multiple of 256"):
         qe.launch_gemm_prefill_w4a16_tiled(tw, ts, dev(A), None, b, M, 64, 128)
