@@ -145,6 +145,12 @@ int qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(const uint16_t* input, cons
  * reference (its GEMMs never split K). */
 int qe_gemm_reserve_workspace(hipStream_t stream);
 
+/* The tile (1 64x64, 2 64x128, 3 128x64, 4 128x128) and K-slice count a
+ * prefill GEMM of this shape would use on the current device with a stream
+ * workspace (tiled != 0: the tiled-layout launchers), after the qe_set_tuning
+ * overrides.  Host only; no counterpart in the reference. */
+int qe_gemm_prefill_plan(int M, int N, int K, int tiled, int* tile, int* slices);
+
 /* Replaces launch_gemm_prefill_w4a16, include/kernels.cuh:119-130.
  * Y[M,N] = fp16(A[M,K] . dequant(W)[N,K]^T), fp32 accumulation;
  * residual added as fp16(fp16(acc) + residual).  `sm_count` is accepted for

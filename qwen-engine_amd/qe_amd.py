@@ -64,6 +64,7 @@ OTHER_SIGNATURES = {
     "qe_gemm_reserve_workspace": [_P],
     "qe_w4_tiled_bytes": [_I, _I, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
     "qe_repack_w4_tiled": [_P, _P, _I, _I, _P, _P, _P],
+    "qe_gemm_prefill_plan": [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)],
 }
 
 ENGINE_SIGNATURES = {
@@ -509,6 +510,13 @@ def stream_read(data, nbytes: int, sink, stream=None):
 
 def gemm_reserve_workspace(stream=None):
     _check(lib().qe_gemm_reserve_workspace(_stream(stream)), "qe_gemm_reserve_workspace")
+
+
+def gemm_prefill_plan(M, N, K, tiled=False):
+    """(tile, slices) a prefill GEMM of this shape would use (qe_gemm_prefill_plan)."""
+    t, sl = ctypes.c_int(), ctypes.c_int()
+    _check(lib().qe_gemm_prefill_plan(M, N, K, int(tiled), ctypes.byref(t), ctypes.byref(sl)), "qe_gemm_prefill_plan")
+    return t.value, sl.value
 
 
 def set_tuning(key: str, value: int):

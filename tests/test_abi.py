@@ -115,3 +115,33 @@ def test_cpp_wrappers_throw(tmp_path):
     assert r.returncode == 0, r.stderr
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+def test_gemm_plan_policy():
+    """The prefill GEMM planner (host code): K slices only where the tile grid
+    leaves CUs idle, never more slices than whole 256-k quads allow with at
+    least 4 steps each, the gemm_tile / gemm_slices overrides honoured, and
+    no K slices when split-K is switched off."""
+    import qe_amd
+    shapes = [(M, N, K) for M in (1, 128, 512, 1024, 2048) for N, K in ((2048, 1536), (1536, 1536), (17920, 1536),
+                                                                       (1536, 8960), (130, 384))]
+    for tiled in (False, True):
+        for M, N, K in shapes:
+            tile, sl = qe_amd.gemm_prefill_plan(M, N, K, tiled)
+            assert 1 <= tile <= 4 and sl >= 1
+            KT = K // 64
+            if sl > 1:
+                assert sl <= (KT // 4 if K % 256 == 0 else KT) and KT // sl >= 4
+                bm, bn = ((64, 64), (64, 128), (128, 64), (128, 128))[tile - 1]
+                assert ((M + bm - 1) // bm) * ((N + bn - 1) // bn) < 2 * 256  # small grids only
+    try:
+        qe_amd.set_tuning("gemm_tile", 3)
+        qe_amd.set_tuning("gemm_slices", 2)
+        assert qe_amd.gemm_prefill_plan(128, 1536, 1536) == (3, 2)
+        qe_amd.set_tuning("gemm_slices", 0)
+        qe_amd.set_tuning("gemm_split_k", 0)
+        assert qe_amd.gemm_prefill_plan(128, 1536, 8960)[1] == 1
+    finally:
+        qe_amd.set_tuning("gemm_tile", 0)
+        qe_amd.set_tuning("gemm_slices", 0)
+        qe_amd.set_tuning("gemm_split_k", 1)
