@@ -333,6 +333,26 @@ def main():
                     gemv_bytes(I, H, act="f16"), I * H // 2)
     per.append(c0)
 
+    # the same GEMV kernels on a matrix large enough to amortize the launch
+    # (N = 65536, K = 16384: 536 MB of packed weights), beside the streaming
+    # ceiling at that size: what the kernel reaches when it is not launch-bound
+    KL, NL = 16384, 65536
+    xl = torch.randn(KL, device=dev, generator=gen).half()
+    q8l = torch.empty(KL, dtype=torch.int8, device=dev)
+    xsl = torch.empty(KL // 128, dtype=torch.float32, device=dev)
+    s8l = torch.empty(KL // 8, dtype=torch.int32, device=dev)
+    outl = torch.empty(NL, dtype=torch.float16, device=dev)
+    qe_amd.launch_quantize_fp16_to_q8_1(xl, q8l, xsl, s8l, KL)
+    torch.cuda.synchronize()
+    large = [kernel_gbs(f"gemv_w4a8 {KL}->{NL}", NL, KL,
+                        lambda w, s: qe_amd.launch_gemv_w4a8(w, s, q8l, xsl, s8l, None, outl, NL, KL),
+                        gemv_bytes(NL, KL), NL * KL // 2),
+             kernel_gbs(f"gemv_w4a16 {KL}->{NL}", NL, KL,
+                        lambda w, s: qe_amd.launch_gemv_w4a16(w, s, xl, None, outl, NL, KL),
+                        gemv_bytes(NL, KL, act="f16"), NL * KL // 2)]
+    result["gemv_large"] = large
+    del xl, q8l, xsl, s8l, outl
+
     # achievable ceiling: a launch that only streams the same number of bytes
     sink = torch.zeros(1 << 14, dtype=torch.int32, device=dev)
     ceil = {}
