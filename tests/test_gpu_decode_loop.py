@@ -92,9 +92,12 @@ def _attn_ref(q, kc, vc, seq_len, group):
     return out
 
 
-@pytest.mark.parametrize("seq_pos", [0, 5, 63, 64, 300, 1024, 1100, 4095])
-def test_flash_decode_attention(qe, orc, seq_pos):
-    nq, nkv, D, max_seq = 12, 2, 128, 4096
+@pytest.mark.parametrize("nq,nkv,seq_pos", [(12, 2, p) for p in (0, 5, 63, 64, 300, 1024, 1100, 4095)] +
+                         [(8, 8, 300), (12, 4, 1100), (14, 2, 77), (16, 1, 2000)])
+def test_flash_decode_attention(qe, orc, nq, nkv, seq_pos):
+    """Stage 1 (one block per q head and split) + stage 2 against float64
+    attention, for Qwen2.5-1.5B's 6:1 grouping and groups of 1, 3, 7, 16."""
+    D, max_seq = 128, 4096
     rng = np.random.default_rng(seq_pos)
     q = rng.standard_normal((nq, D)).astype(np.float16)
     kc = rng.standard_normal((nkv, max_seq, D)).astype(np.float16)
