@@ -58,3 +58,17 @@ def test_cpp_api_matrix_path(orc, tmp_path):
     ref, ex, bd = orc.gemm_w4a16(qw, sc, A[:8], 8, N, K)
     assert_fp16_close(gemm[:8], ex, bd, ref, what="C++ launch_gemm_prefill_w4a16")
     assert np.all(np.isfinite(gemm.astype(np.float32)))
+
+
+def test_cpp_api_wrappers_match_c_abi():
+    """Every other qwen:: launcher (embedding, RMSNorm, the quantizer, the
+    SwiGLU GEMVs, the QKV and SwiGLU prefill GEMMs, bias + RoPE + KV append,
+    prefill and decode attention with the Q8_1 epilogue, sampling) writes the
+    same bytes as the qe_ function it wraps on the same inputs, so no wrapper
+    passes an argument in the wrong place.  The qe_ functions themselves are
+    checked against the oracle by the other GPU tests."""
+    if not os.path.exists(EXE):
+        pytest.fail("cpp_api_gpu is not built (make -C qwen-engine_amd)")
+    print("running cpp_api_gpu --wrappers", flush=True)
+    r = subprocess.run([EXE, "--wrappers"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "wrappers ok" in r.stdout, r.stdout + r.stderr
