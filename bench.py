@@ -333,6 +333,28 @@ def main():
                     gemv_bytes(I, H, act="f16"), I * H // 2)
     per.append(c0)
 
+    # one GPU's share of a tensor-parallel decode layer at p = 8 (column shards
+    # of QKV, gate/up and the LM head; row shards of O and down in whole
+    # 128-groups): the kernels the sharded path would run, on one GPU
+    P = 8
+    shard = []
+    kd = -(-(I // 128) // P) * 128   # down: ceil(70 / 8) = 9 groups -> K = 1152
+    ko = 2 * HD                      # O: two of the 12 heads -> K = 256
+    for name, N_, K_, launch_ in (
+            (f"QKV column shard 1536->{(NQ * HD + 2 * NKV * HD) // P}", (NQ * HD + 2 * NKV * HD) // P, H,
+             lambda w, s: qe_amd.launch_gemv_w4a8(w, s, q8, xs, s8, None, mlp, (NQ * HD + 2 * NKV * HD) // P, H)),
+            (f"gate/up column shard 1536->2x{I // P}", 2 * I // P, H,
+             lambda w, s: qe_amd.launch_gemv_dual_gate_up_swiglu_w4a8(w, s, q8, xs, s8, mlp, H, I // P)),
+            (f"down row shard {kd}->1536", H, kd,
+             lambda w, s: qe_amd.launch_gemv_w4a8(w, s, q8, xs, s8, None, hidden, H, kd)),
+            (f"O row shard {ko}->1536", H, ko,
+             lambda w, s: qe_amd.launch_gemv_w4a8(w, s, q8, xs, s8, None, hidden, H, ko)),
+            (f"LM head column shard 1536->{V // P}", V // P, H,
+             lambda w, s: qe_amd.launch_gemv_w4a8(w, s, q8, xs, s8, None, logits, V // P, H))):
+        nb = gemv_bytes(N_, K_, out_n=I // P if name.startswith("gate") else None)
+        shard.append(kernel_gbs("gemv_w4a8 " + name, N_, K_, launch_, nb, N_ * K_ // 2))
+    result["shard_tp8"] = shard
+
     # the same GEMV kernels on a matrix large enough to amortize the launch
     # (N = 65536, K = 16384: 536 MB of packed weights), beside the streaming
     # ceiling at that size: what the kernel reaches when it is not launch-bound
