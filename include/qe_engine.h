@@ -95,6 +95,14 @@ int qe_engine_read_hidden(qe_engine* e, uint16_t* host, int n);
  * gate_up_w gate_up_s down_w down_s q_bias k_bias v_bias. */
 int qe_engine_read_buffer(qe_engine* e, const char* name, void* host, size_t bytes);
 
+/* The arena layout: every buffer the engine carved out of its one device
+ * allocation, in allocation order, as (offset, bytes) pairs; *count receives
+ * the number of buffers (at most `capacity` are written), *arena_bytes the
+ * allocation's size.  For layout checks like the reference's scratch
+ * non-overlap test (tests/test_kernels.cu:687-705); host only. */
+int qe_engine_arena_spans(const qe_engine* e, size_t* offsets, size_t* sizes, int capacity, int* count,
+                          size_t* arena_bytes);
+
 #ifdef __cplusplus
 }
 #endif

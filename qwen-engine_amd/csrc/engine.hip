@@ -104,10 +104,12 @@ struct qe_engine {
     int seq_pos = 0;
     bool tiled = false;  // prefill GEMMs read the tiled copies
 
+    std::vector<std::pair<size_t, size_t>> spans;  // (offset, bytes) of every buffer taken
     template <class T>
     T* take(size_t bytes) {
         size_t off = qe::align256(arena_used);
         arena_used = off + bytes;
+        spans.emplace_back(off, bytes);
         return reinterpret_cast<T*>(arena + off);
     }
     size_t kv_stride() const { return static_cast<size_t>(cfg.num_kv_heads) * cfg.max_seq_len * cfg.head_dim; }
@@ -788,6 +790,20 @@ extern "C" int qe_engine_read_hidden(qe_engine* e, uint16_t* host, int n) {
     QE_REQUIRE(e && host && n >= 0 && n <= e->cfg.hidden_size * e->cfg.prefill_chunk, "engine_read_hidden: bad arguments");
     QE_HIP(hipStreamSynchronize(e->stream));
     QE_HIP(hipMemcpy(host, e->act0, static_cast<size_t>(n) * 2, hipMemcpyDeviceToHost));
+    return QE_OK;
+}
+
+extern "C" int qe_engine_arena_spans(const qe_engine* e, size_t* offsets, size_t* sizes, int capacity, int* count,
+                                     size_t* arena_bytes) {
+    QE_REQUIRE(e && count && capacity >= 0 && (capacity == 0 || (offsets && sizes)),
+               "engine_arena_spans: bad arguments");
+    const int n = static_cast<int>(e->spans.size());
+    for (int i = 0; i < n && i < capacity; ++i) {
+        offsets[i] = e->spans[i].first;
+        sizes[i] = e->spans[i].second;
+    }
+    *count = n;
+    if (arena_bytes) *arena_bytes = e->arena_size;
     return QE_OK;
 }
 

@@ -77,6 +77,7 @@ ENGINE_SIGNATURES = {
     "qe_engine_read_logits": [_P, _P, _I],
     "qe_engine_read_hidden": [_P, _P, _I],
     "qe_engine_read_buffer": [_P, ctypes.c_char_p, _P, ctypes.c_size_t],
+    "qe_engine_arena_spans": [_P, _P, _P, _I, _P, _P],
     "qe_engine_create_from_qwenbin": [ctypes.c_char_p, _I, _I, _I, _P],
     "qe_engine_save_qwenbin": [_P, ctypes.c_char_p],
     "qe_qwenbin_inspect": [ctypes.c_char_p, _P],
@@ -489,6 +490,17 @@ class Engine:
         out = np.empty(self.cfg.hidden_size, np.float16)
         _check(lib().qe_engine_read_hidden(self._h, out.ctypes.data, out.size), "qe_engine_read_hidden")
         return out
+
+    def arena_spans(self):
+        """[(offset, bytes)] of every buffer in the engine's arena, in allocation
+        order, and the arena's size (qe_engine_arena_spans)."""
+        n, total = ctypes.c_int(), ctypes.c_size_t()
+        _check(lib().qe_engine_arena_spans(self._h, None, None, 0, ctypes.byref(n), ctypes.byref(total)),
+               "qe_engine_arena_spans")
+        offs, sizes = (ctypes.c_size_t * max(n.value, 1))(), (ctypes.c_size_t * max(n.value, 1))()
+        _check(lib().qe_engine_arena_spans(self._h, offs, sizes, n.value, ctypes.byref(n), None),
+               "qe_engine_arena_spans")
+        return list(zip(offs[:n.value], sizes[:n.value])), total.value
 
     def read(self, name: str, dtype, count: int):
         """Copy of the first `count` elements of a named engine buffer."""

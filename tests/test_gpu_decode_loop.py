@@ -329,3 +329,26 @@ def test_engine_tiled_prefill_matches_qwenbin_layout(qe):
     assert np.array_equal(outs[0][1], outs[1][1])
     assert np.array_equal(outs[0][2], outs[1][2])
     assert outs[0][3] == outs[1][3]
+
+
+@pytest.mark.parametrize("full", [False, True])
+def test_engine_arena_buffers_do_not_overlap(qe, full):
+    """Every buffer carved out of the engine's arena (weights, tiled copies,
+    KV cache, activations, the Q8_1 scratch, partials, control block) starts
+    on a 256-byte boundary, ends before the next one starts and inside the
+    allocation - the layout property of the reference's scratch non-overlap
+    test (tests/test_kernels.cu:687-705), for a small model and the full
+    Qwen2.5-1.5B configuration."""
+    cfg = qe.default_config() if full else _small_cfg(qe)
+    e = qe.Engine(cfg, seed=3)
+    spans, total = e.arena_spans()
+    e.close()
+    assert len(spans) > 20
+    ends = 0
+    for off, size in spans:  # allocation order = address order
+        assert off % 256 == 0 and size > 0
+        assert off >= ends, (off, ends)
+        ends = off + size
+    assert ends <= total
+    if full:  # 28 layers x (2 norms, 3 biases, 6 matrices x (weights, scales) and their tiled copies)
+        assert len(spans) >= 28 * (5 + 12 + 12)
