@@ -352,3 +352,23 @@ def test_engine_arena_buffers_do_not_overlap(qe, full):
     assert ends <= total
     if full:  # 28 layers x (2 norms, 3 biases, 6 matrices x (weights, scales) and their tiled copies)
         assert len(spans) >= 28 * (5 + 12 + 12)
+
+
+def test_engine_profile_decode_stages(qe):
+    """Per-stage timing of one eager decode step (the reference's
+    profile_stages positivity check, tests/test_kernels.cu:708-719): every
+    stage positive, the total their sum, one position consumed, and the next
+    graph step still matches a fresh engine's."""
+    prompt = [(i % 1000) + 100 for i in range(24)]
+    e = qe.Engine(_small_cfg(qe), seed=5)
+    e.prefill(prompt)
+    prof = e.profile_decode()
+    assert prof["gemv_ms"] > 0 and prof["attention_ms"] > 0 and prof["other_ms"] > 0
+    assert abs(prof["total_ms"] - (prof["gemv_ms"] + prof["attention_ms"] + prof["other_ms"])) < 1e-3
+    assert e.seq_pos == len(prompt) + 1
+    after = e.decode(3)
+    ref = qe.Engine(_small_cfg(qe), seed=5)
+    ref.prefill(prompt)
+    assert ref.decode(4)[1:] == after
+    e.close()
+    ref.close()
