@@ -5,6 +5,7 @@
 // operations instead of warp shuffles, wave64 lanes.  HIP device code only.
 #pragma once
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -124,6 +125,23 @@ __device__ __forceinline__ Q8Group quantize_group128_q8_1(const float vals[8]) {
     return g;
 }
 
+// quantize_group128_fp16_to_q8_1 (reference quant_primitives.cuh:37-89): the
+// reference's entry point, same parameters and meaning.  The 16 lanes of a
+// 128-element group (an aligned DPP row, all 16 active) each pass their 8
+// values; lane `sub_lane` (0..15) of group `group_idx` stores its 8 q8 bytes
+// at out_q8[128*group_idx + 8*sub_lane] (one 8-byte store) and its sum8 at
+// out_sum8[16*group_idx + sub_lane]; sub_lane 0 stores the scale d at
+// out_scale[group_idx].  A nullptr output is skipped.  Rounding is the CPU
+// golden's (half away from zero), see quantize_group128_q8_1.
+__device__ __forceinline__ void quantize_group128_fp16_to_q8_1(const float vals[8], int group_idx, int sub_lane,
+                                                               int8_t* out_q8, float* out_scale, int32_t* out_sum8) {
+    const Q8Group g = quantize_group128_q8_1(vals);
+    if (out_q8 != nullptr)
+        *reinterpret_cast<int2*>(out_q8 + static_cast<size_t>(group_idx) * 128 + sub_lane * 8) = make_int2(g.x_lo, g.x_hi);
+    if (out_sum8 != nullptr) out_sum8[static_cast<size_t>(group_idx) * 16 + sub_lane] = g.sum8;
+    if (out_scale != nullptr && sub_lane == 0) out_scale[group_idx] = g.d;
+}
+
 // ---- int4 -> fp16 dequantization -------------------------------------------
 // unpack_w4_to_half2_quad (reference quant_primitives.cuh:92-115): the 8
 // elements of a packed word in K order, (q-8)*scale with one fp16 RNE
@@ -147,6 +165,16 @@ __device__ __forceinline__ qe_half8_t unpack_w4_to_half8(uint32_t packed, _Float
     qe_half2_t h45 = (__builtin_bit_cast(qe_half2_t, u45) - b) * s;
     qe_half2_t h67 = (__builtin_bit_cast(qe_half2_t, u67) - b) * s;
     return qe_half8_t{h01[0], h01[1], h23[0], h23[1], h45[0], h45[1], h67[0], h67[1]};
+}
+
+// unpack_w4_to_half2_quad (reference quant_primitives.cuh:92-115): the
+// reference's entry point, same parameters and meaning: out_h2[i] holds
+// elements (2i, 2i+1) of the word in K order, each (q-8)*scale rounded once
+// to fp16 (RNE).  Same arithmetic as unpack_w4_to_half8.
+__device__ __forceinline__ void unpack_w4_to_half2_quad(uint32_t packed, half scale, half2 out_h2[4]) {
+    const qe_half8_t h = unpack_w4_to_half8(packed, __builtin_bit_cast(_Float16, scale));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out_h2[i] = __builtin_bit_cast(half2, qe_half2_t{h[2 * i], h[2 * i + 1]});
 }
 
 }  // namespace qwen
