@@ -91,9 +91,16 @@ def main():
     def copies_for(nbytes):
         return max(2, -(-POOL_BYTES // nbytes))
 
+    # one capture stream for every graph, holding a split-K workspace (the
+    # prefill GEMMs split K only on streams that hold one); eager launches run
+    # on the default stream, which holds one too
+    cap_stream = torch.cuda.Stream()
+    qe_amd.gemm_reserve_workspace(cap_stream)
+    qe_amd.gemm_reserve_workspace()
+
     def graph_of(fn, reps):
         """Capture fn(i) for i in range(reps) into one graph."""
-        s = torch.cuda.Stream()
+        s = cap_stream
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             for i in range(min(reps, 3)):
@@ -101,7 +108,6 @@ def main():
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
-        # capture on the warm-up stream: it already holds the split-K workspace
         with torch.cuda.graph(g, stream=s):
             for i in range(reps):
                 fn(i)

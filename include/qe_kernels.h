@@ -12,14 +12,18 @@
  *   - `stream` is a hipStream_t (NULL = the null stream).
  * Every call is asynchronous on `stream`, never synchronizes, and is safe
  * under HIP graph capture.  `residual` may alias the output.  A NULL
- * optional pointer means "skip", as in the reference.  No call allocates,
- * except that the prefill GEMMs, when they split K over several blocks,
- * keep fp32 partial sums in a 32 MiB workspace that belongs to the stream:
- * the first such launch on a stream allocates it (hipMalloc, outside graph
- * capture only) and it is kept until the process ends.  GEMMs on different
- * streams therefore never share partials.  A launch being captured on a
- * stream that has no workspace yet runs without K slices (same results,
- * different speed); qe_gemm_reserve_workspace() allocates one ahead.
+ * optional pointer means "skip", as in the reference.  No launcher
+ * allocates (the reference's launchers keep no state and allocate nothing,
+ * src/kernels/gemm_prefill.cu:616-684).  The prefill GEMMs may split K over
+ * several blocks and then keep fp32 partial sums in a workspace registered
+ * for the launching stream, ahead of time, by qe_gemm_reserve_workspace (the
+ * library allocates 32 MiB) or qe_gemm_attach_workspace (caller memory).  A
+ * stream without a workspace runs its GEMMs without K slices, eagerly and
+ * under graph capture alike: the plan, and so the bits, of a launch depend
+ * only on the shape, the qe_set_tuning switches and whether the stream holds
+ * a workspace.  GEMMs on different streams never share partials.
+ * hipStreamPerThread never holds a workspace (it names a different stream
+ * in every thread); the null stream is the device's legacy stream.
  *
  * Return value: QE_OK, or a QE_ERR_* code; qe_last_error() then describes
  * the failure (thread-local).  The C++ mirror in kernels.hpp turns a
@@ -137,13 +141,30 @@ int qe_launch_rmsnorm_gemv_dual_gate_up_swiglu_w4a16(const uint16_t* input, cons
 
 /* ---- prefill dequant-GEMM (MFMA) ----------------------------------------- */
 
-/* Allocates the split-K workspace of `stream` on the current device now (it
- * is otherwise allocated by the first prefill GEMM on the stream that runs
- * outside graph capture).  Call it before capturing prefill GEMMs into a
- * graph on a new stream.  At most 64 streams per device hold one; later
- * streams run their GEMMs without K slices.  No counterpart in the
+/* Allocates a 32 MiB split-K workspace for `stream` on the current device
+ * (hipMalloc; the only allocation of the kernel API) and registers it, so
+ * prefill GEMMs on that stream may split K.  Call it before the first GEMM
+ * on the stream, outside graph capture (QE_ERR_INVALID_ARGUMENT while the
+ * stream is capturing, or for hipStreamPerThread).  At most 64 streams per
+ * device hold a workspace (QE_ERR_UNSUPPORTED beyond).  No counterpart in the
  * reference (its GEMMs never split K). */
 int qe_gemm_reserve_workspace(hipStream_t stream);
+
+/* Registers caller memory (>= 1 MiB, 256-byte aligned; at most 32 MiB is
+ * used) as the split-K workspace of `stream` on the current device, in place
+ * of one allocated by qe_gemm_reserve_workspace (which is then freed).  The
+ * memory must stay valid until qe_gemm_release_workspace(stream).  No
+ * counterpart in the reference. */
+int qe_gemm_attach_workspace(hipStream_t stream, void* workspace, size_t bytes);
+
+/* Drops the workspace of `stream` on the current device (freed if the
+ * library allocated it; call it before destroying the stream).  Later GEMMs
+ * on the stream run without K slices.  QE_OK also when there was none. */
+int qe_gemm_release_workspace(hipStream_t stream);
+
+/* Number of hipMalloc calls the library has made for GEMM workspaces in this
+ * process (only qe_gemm_reserve_workspace makes them).  Test hook. */
+long qe_gemm_workspace_allocations(void);
 
 /* The tile (1 64x64, 2 64x128, 3 128x64, 4 128x128) and K-slice count a
  * prefill GEMM of this shape would use on the current device with a stream
@@ -156,13 +177,14 @@ int qe_gemm_prefill_plan(int M, int N, int K, int tiled, int* tile, int* slices)
  * residual added as fp16(fp16(acc) + residual).  `sm_count` is accepted for
  * signature parity; tile selection uses the device's CU count.  K-slice
  * partials are summed in slice order, so a given plan is deterministic; a
- * launch without a workspace (see above) may round differently in fp32. */
+ * stream without a workspace (see above) runs unsplit, which may round
+ * differently in fp32 from a split plan. */
 int qe_launch_gemm_prefill_w4a16(const uint32_t* qweight, const uint16_t* scales, const uint16_t* input_x,
                                  const uint16_t* residual, uint16_t* output_y, int M, int N, int K,
                                  hipStream_t stream, int sm_count);
 
 /* qe_launch_gemm_prefill_w4a16 without any allocation, for callers that
- * cannot allocate (code under graph capture on a stream with no workspace,
+ * cannot allocate or register a workspace (code under graph capture,
  * serving loops, harnesses that forbid hipMalloc).  No counterpart in the
  * reference.  Same arguments, same tile and K-slice plan and same results as
  * qe_launch_gemm_prefill_w4a16; the split-K partials go to a 32 MiB device

@@ -102,7 +102,9 @@ struct qe_engine {
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     int seq_pos = 0;
-    bool tiled = false;  // prefill GEMMs read the tiled copies
+    bool tiled = false;        // prefill GEMMs read the tiled copies
+    bool want_tiled = false;   // engine_tiled_prefill, read once at create
+    float* gemm_ws = nullptr;  // split-K workspace of the engine's stream (in the arena)
 
     std::vector<std::pair<size_t, size_t>> spans;  // (offset, bytes) of every buffer taken
     template <class T>
@@ -344,7 +346,10 @@ extern "C" void qe_engine_destroy(qe_engine* e) {
     if (e->h_token) (void)hipHostFree(e->h_token);
     if (e->arena) (void)hipFree(e->arena);
     if (e->payload) (void)hipFree(e->payload);
-    if (e->stream) (void)hipStreamDestroy(e->stream);
+    if (e->stream) {
+        if (e->gemm_ws) (void)qe_gemm_release_workspace(e->stream);
+        (void)hipStreamDestroy(e->stream);
+    }
     delete e;
 }
 
@@ -375,14 +380,14 @@ size_t tiled_mat_bytes(int rows, int K) {
     return align256(w) + align256(sb);
 }
 
-bool tiled_ok(const qe_engine_config& c) {
+bool tiled_ok(const qe_engine_config& c, bool want_tiled) {
     const int qd = c.num_q_heads * c.head_dim, kvd = c.num_kv_heads * c.head_dim;
-    return engine_tiled_prefill() && c.hidden_size % 256 == 0 && c.intermediate_size % 256 == 0 && qd % 256 == 0 &&
+    return want_tiled && c.hidden_size % 256 == 0 && c.intermediate_size % 256 == 0 && qd % 256 == 0 &&
            qd % 32 == 0 && kvd % 32 == 0;
 }
 
-size_t tiled_bytes(const qe_engine_config& c) {
-    if (!tiled_ok(c)) return 0;
+size_t tiled_bytes(const qe_engine_config& c, bool want_tiled) {
+    if (!tiled_ok(c, want_tiled)) return 0;
     const int H = c.hidden_size, I = c.intermediate_size, qd = c.num_q_heads * c.head_dim,
               kvd = c.num_kv_heads * c.head_dim;
     return static_cast<size_t>(c.num_layers) *
@@ -393,7 +398,7 @@ size_t tiled_bytes(const qe_engine_config& c) {
 // Carves the tiled copies out of the arena and writes them (on the engine's
 // stream, after the weights are in place).
 int setup_tiled(qe_engine* e) {
-    if (!tiled_ok(e->cfg)) return QE_OK;
+    if (!tiled_ok(e->cfg, e->want_tiled)) return QE_OK;
     auto tile = [&](const Mat& m, Mat& t) -> int {
         size_t wb = 0, sb = 0;
         QE_TRY(qe_w4_tiled_bytes(m.rows, m.K, &wb, &sb));
@@ -421,7 +426,11 @@ int q8_len(const qe_engine_config& c) {
     return std::max(c.intermediate_size, std::max(c.hidden_size, c.num_q_heads * c.head_dim));
 }
 
-size_t workspace_bytes(const qe_engine_config& c) {
+// The engine's split-K workspace for its prefill GEMMs (registered for the
+// engine's stream with qe_gemm_attach_workspace, released at destroy).
+constexpr size_t kEngineGemmWsBytes = size_t(32) << 20;
+
+size_t workspace_bytes(const qe_engine_config& c, bool want_tiled) {
     const int H = c.hidden_size, I = c.intermediate_size, qd = c.num_q_heads * c.head_dim,
               kvd = c.num_kv_heads * c.head_dim, T = c.prefill_chunk, QN = q8_len(c);
     size_t bytes = 2 * align256(static_cast<size_t>(c.num_layers) * c.num_kv_heads * c.max_seq_len * c.head_dim * 2);
@@ -431,12 +440,13 @@ size_t workspace_bytes(const qe_engine_config& c) {
     bytes += align256(QN) + align256(QN / 128 * 4) + align256(QN / 8 * 4);
     bytes += 2 * align256(static_cast<size_t>(c.num_q_heads) * 16 * 128 * 4) +
              2 * align256(QE_LM_HEAD_SAMPLE_PARTS * 4) + align256(static_cast<size_t>(c.max_seq_len) * 4) + 256 +
-             256 + 4096;
-    return bytes + tiled_bytes(c);
+             256 + 4096 + kEngineGemmWsBytes;
+    return bytes + tiled_bytes(c, want_tiled);
 }
 
-int begin_engine(qe_engine* e, const qe_engine_config& c, size_t arena_bytes) {
+int begin_engine(qe_engine* e, const qe_engine_config& c, bool want_tiled, size_t arena_bytes) {
     e->cfg = c;
+    e->want_tiled = want_tiled;
     QE_HIP(hipStreamCreate(&e->stream));
     QE_HIP(hipMalloc(&e->arena, arena_bytes));
     e->arena_size = arena_bytes;
@@ -469,6 +479,7 @@ void layout_workspace(qe_engine* e) {
     e->sample_idx = e->take<int32_t>(QE_LM_HEAD_SAMPLE_PARTS * 4);
     e->tokens = e->take<int32_t>(static_cast<size_t>(c.max_seq_len) * 4);
     e->ctl = e->take<qe_device_control_block>(sizeof(qe_device_control_block));
+    e->gemm_ws = e->take<float>(kEngineGemmWsBytes);
 }
 
 // KV cache cleared, control block at position 0, decode graph captured
@@ -476,6 +487,7 @@ int finish_engine(qe_engine* e) {
     QE_TRY(setup_tiled(e));
     QE_REQUIRE(e->arena_used <= e->arena_size, "engine_create: arena overflow (%zu > %zu)", e->arena_used,
                e->arena_size);
+    QE_TRY(qe_gemm_attach_workspace(e->stream, e->gemm_ws, kEngineGemmWsBytes));
     (void)cu_count();  // cache the device fact before graph capture
     const size_t kvb = static_cast<size_t>(e->cfg.num_layers) * e->kv_stride() * 2;
     QE_HIP(hipMemsetAsync(e->kcache, 0, kvb, e->stream));
@@ -495,7 +507,8 @@ extern "C" int qe_engine_create(const qe_engine_config* cfg, uint64_t seed, qe_e
     const qe_engine_config& c = *cfg;
     QE_REQUIRE(config_ok(c), "engine_create: unsupported configuration");
     std::unique_ptr<qe_engine, void (*)(qe_engine*)> e(new qe_engine(), qe_engine_destroy);
-    QE_TRY(begin_engine(e.get(), c, weight_bytes(c) + workspace_bytes(c)));
+    const bool want_tiled = engine_tiled_prefill() != 0;
+    QE_TRY(begin_engine(e.get(), c, want_tiled, weight_bytes(c) + workspace_bytes(c, want_tiled)));
     const int H = c.hidden_size, I = c.intermediate_size, qd = c.num_q_heads * c.head_dim,
               kvd = c.num_kv_heads * c.head_dim;
     // layout first, then check, then initialize
@@ -564,7 +577,8 @@ extern "C" int qe_engine_create_from_qwenbin(const char* path, int max_seq_len, 
     c.fused_decode = fused_decode;
     QE_REQUIRE(config_ok(c), "engine_create_from_qwenbin: unsupported configuration");
     std::unique_ptr<qe_engine, void (*)(qe_engine*)> e(new qe_engine(), qe_engine_destroy);
-    QE_TRY(begin_engine(e.get(), c, workspace_bytes(c)));
+    const bool want_tiled = engine_tiled_prefill() != 0;
+    QE_TRY(begin_engine(e.get(), c, want_tiled, workspace_bytes(c, want_tiled)));
     // one device copy of the payload [weights_offset, end of file) (src/engine.cu:271-272)
     QE_HIP(hipMalloc(&e->payload, std::max<uint64_t>(in.weights_bytes, 256)));
     QE_HIP(hipMemcpy(e->payload, file.data() + in.weights_offset, in.weights_bytes, hipMemcpyHostToDevice));

@@ -23,6 +23,7 @@
 //     (blocks per CU, steps per block, split-K overhead); split-K partials
 //     are reduced by a second kernel in slice order.
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "qe_common.hpp"
@@ -68,6 +69,11 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // (gemm_workspace below), so GEMMs in flight on different streams never
 // share partials.
 constexpr size_t kWsFloats = size_t(8) << 20;  // 32 MiB
+
+struct Workspace {
+    float* ptr = nullptr;
+    size_t floats = 0;
+};
 
 // One 32x32 accumulator fragment whose rows start at r0 and whose lane
 // column is col.  D[i][j] of a 32x32 MFMA tile: j = lane%32,
@@ -747,10 +753,10 @@ void plan_gemm(int M, int N, int K, size_t ws_floats, bool tiled, int& ti, int& 
 }
 
 template <int MODE>
-int launch_gemm(GemmParams p, hipStream_t stream, const char* what, float* ws, size_t ws_floats, bool tiled = false) {
+int launch_gemm(GemmParams p, hipStream_t stream, const char* what, Workspace ws, bool tiled = false) {
     if (p.M <= 0 || p.N <= 0) return QE_OK;
-    p.ws = ws;
-    if (ws == nullptr) ws_floats = 0;
+    p.ws = ws.ptr;
+    const size_t ws_floats = ws.ptr == nullptr ? 0 : ws.floats;
     int ti = 0, slices = 1;
     plan_gemm(p.M, p.N, p.K, ws_floats, tiled, ti, slices);
     const TileCost& t = kTiles[ti];
@@ -926,10 +932,10 @@ __global__ __launch_bounds__(256, 2) void gemm_w4a8_mfma_kernel(GemmParams p) {
 }
 
 template <int MODE>
-int launch_gemm_w4a8(GemmParams p, hipStream_t stream, const char* what, float* ws, size_t ws_floats) {
+int launch_gemm_w4a8(GemmParams p, hipStream_t stream, const char* what, Workspace ws) {
     if (p.M <= 0 || p.N <= 0) return QE_OK;
-    p.ws = ws;
-    if (ws == nullptr) ws_floats = 0;
+    p.ws = ws.ptr;
+    const size_t ws_floats = ws.ptr == nullptr ? 0 : ws.floats;
     // 128-row tiles when they already give one block per CU, else 64-row tiles
     const int cus = cu_count();
     const int nt128 = ((p.M + 127) / 128) * ((p.N + 127) / 128);
@@ -987,52 +993,140 @@ __global__ __launch_bounds__(256) void repack_w4_tiled_kernel(const u32x4* __res
     }
 }
 
-// The split-K workspace of `stream` on the current device: allocated by the
-// first launch on that stream that is not being captured into a graph, then
-// kept until the process ends (at most kMaxWsStreams per device; further
-// streams and captures on a stream without one run without K slices).
+// Split-K workspaces, one per (device, stream).  A launch only looks its
+// stream's workspace up and never allocates: a stream without one runs its
+// GEMMs without K slices, eagerly and under capture alike, so the plan and
+// the bits of a launch depend only on the shape, the tuning switches and
+// whether the stream holds a workspace.  qe_gemm_reserve_workspace
+// allocates one (the library owns it), qe_gemm_attach_workspace registers
+// caller memory (the engine's arena), qe_gemm_release_workspace drops the
+// entry.  hipStreamPerThread names a different stream in each thread, so it
+// never holds a workspace (its GEMMs run unsplit); the null stream is the one
+// legacy stream of the device (this library is built without per-thread
+// default streams), shared correctly ordered by every thread.
 constexpr int kMaxWsStreams = 64;
 struct WsSlot {
     hipStream_t stream;
     float* ptr;
+    size_t floats;
+    bool owned;  // allocated by qe_gemm_reserve_workspace
 };
 std::mutex g_ws_mutex;
 WsSlot g_ws[64][kMaxWsStreams];
 int g_ws_count[64];
+std::atomic<long> g_ws_allocations{0};  // hipMalloc calls made for workspaces
 
-float* gemm_workspace(hipStream_t stream) {
-    if (!gemm_split_k_enabled()) return nullptr;
+bool per_thread_handle(hipStream_t stream) { return stream == hipStreamPerThread; }
+
+Workspace gemm_workspace(hipStream_t stream) {
+    if (!gemm_split_k_enabled() || per_thread_handle(stream)) return {};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return {};
+    }
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     for (int i = 0; i < g_ws_count[dev]; ++i)
-        if (g_ws[dev][i].stream == stream) return g_ws[dev][i].ptr;
+        if (g_ws[dev][i].stream == stream) return {g_ws[dev][i].ptr, g_ws[dev][i].floats};
+    return {};
+}
+
+// registers (ptr, floats) for `stream` on the current device; the caller
+// holds g_ws_mutex.  Returns the slot or nullptr when the table is full.
+WsSlot* ws_find_or_add(int dev, hipStream_t stream, bool* found) {
+    for (int i = 0; i < g_ws_count[dev]; ++i)
+        if (g_ws[dev][i].stream == stream) {
+            *found = true;
+            return &g_ws[dev][i];
+        }
+    *found = false;
     if (g_ws_count[dev] == kMaxWsStreams) return nullptr;
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &st) != hipSuccess || st != hipStreamCaptureStatusNone) {
+    WsSlot* s = &g_ws[dev][g_ws_count[dev]++];
+    *s = WsSlot{stream, nullptr, 0, false};
+    return s;
+}
+
+int current_device(const char* what, int* dev) {
+    if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= 64) {
         (void)hipGetLastError();
-        return nullptr;
+        return fail(QE_ERR_HIP, "%s: no current device", what);
     }
-    void* ptr = nullptr;
-    if (hipMalloc(&ptr, kWsFloats * sizeof(float)) != hipSuccess) {
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    g_ws[dev][g_ws_count[dev]++] = WsSlot{stream, static_cast<float*>(ptr)};
-    return static_cast<float*>(ptr);
+    return QE_OK;
 }
 
 }  // namespace
 }  // namespace qe
 
 extern "C" int qe_gemm_reserve_workspace(hipStream_t stream) {
-    if (!qe::gemm_split_k_enabled()) return QE_OK;
-    if (qe::gemm_workspace(stream) == nullptr)
-        return qe::fail(QE_ERR_HIP, "gemm_reserve_workspace: no workspace (stream capturing, allocation failed or "
-                                    "%d streams already hold one)", qe::kMaxWsStreams);
+    const char* what = "gemm_reserve_workspace";
+    QE_REQUIRE(!qe::per_thread_handle(stream), "%s: hipStreamPerThread cannot hold a workspace (its GEMMs run "
+               "without K slices)", what);
+    int dev = 0;
+    QE_TRY(qe::current_device(what, &dev));
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return qe::fail(QE_ERR_HIP, "%s: invalid stream", what);
+    }
+    QE_REQUIRE(st == hipStreamCaptureStatusNone, "%s: stream is capturing", what);
+    std::lock_guard<std::mutex> lock(qe::g_ws_mutex);
+    bool found = false;
+    qe::WsSlot* s = qe::ws_find_or_add(dev, stream, &found);
+    if (s == nullptr)
+        return qe::fail(QE_ERR_UNSUPPORTED, "%s: %d streams already hold a workspace on this device", what,
+                        qe::kMaxWsStreams);
+    if (found && s->floats >= qe::kWsFloats) {
+        qe::clear_error();
+        return QE_OK;
+    }
+    void* ptr = nullptr;
+    ++qe::g_ws_allocations;
+    if (hipMalloc(&ptr, qe::kWsFloats * sizeof(float)) != hipSuccess) {
+        (void)hipGetLastError();
+        if (!found) --qe::g_ws_count[dev];
+        return qe::fail(QE_ERR_HIP, "%s: hipMalloc of %zu bytes failed", what, qe::kWsFloats * sizeof(float));
+    }
+    if (found && s->owned) (void)hipFree(s->ptr);
+    *s = qe::WsSlot{stream, static_cast<float*>(ptr), qe::kWsFloats, true};
     qe::clear_error();
     return QE_OK;
 }
+
+extern "C" int qe_gemm_attach_workspace(hipStream_t stream, void* workspace, size_t bytes) {
+    const char* what = "gemm_attach_workspace";
+    QE_REQUIRE(!qe::per_thread_handle(stream), "%s: hipStreamPerThread cannot hold a workspace", what);
+    QE_REQUIRE(workspace != nullptr && qe::aligned(workspace, 256), "%s: workspace must be non-NULL and "
+               "256-byte aligned", what);
+    QE_REQUIRE(bytes >= (size_t(1) << 20), "%s: %zu bytes is below the 1 MiB minimum", what, bytes);
+    int dev = 0;
+    QE_TRY(qe::current_device(what, &dev));
+    std::lock_guard<std::mutex> lock(qe::g_ws_mutex);
+    bool found = false;
+    qe::WsSlot* s = qe::ws_find_or_add(dev, stream, &found);
+    if (s == nullptr)
+        return qe::fail(QE_ERR_UNSUPPORTED, "%s: %d streams already hold a workspace on this device", what,
+                        qe::kMaxWsStreams);
+    if (found && s->owned) (void)hipFree(s->ptr);
+    *s = qe::WsSlot{stream, static_cast<float*>(workspace), std::min(bytes / sizeof(float), qe::kWsFloats), false};
+    qe::clear_error();
+    return QE_OK;
+}
+
+extern "C" int qe_gemm_release_workspace(hipStream_t stream) {
+    int dev = 0;
+    QE_TRY(qe::current_device("gemm_release_workspace", &dev));
+    std::lock_guard<std::mutex> lock(qe::g_ws_mutex);
+    for (int i = 0; i < qe::g_ws_count[dev]; ++i)
+        if (qe::g_ws[dev][i].stream == stream) {
+            if (qe::g_ws[dev][i].owned) (void)hipFree(qe::g_ws[dev][i].ptr);
+            qe::g_ws[dev][i] = qe::g_ws[dev][--qe::g_ws_count[dev]];
+            break;
+        }
+    qe::clear_error();
+    return QE_OK;
+}
+
+extern "C" long qe_gemm_workspace_allocations(void) { return qe::g_ws_allocations.load(); }
 
 namespace qe {
 namespace {
@@ -1091,7 +1185,7 @@ extern "C" int qe_launch_gemm_prefill_w4a16(const uint32_t* qweight, const uint1
     p.M = M;
     p.N = N;
     p.K = K;
-    return launch_gemm<kPlain>(p, stream, what, gemm_workspace(stream), kWsFloats);
+    return launch_gemm<kPlain>(p, stream, what, gemm_workspace(stream));
 }
 
 extern "C" int qe_launch_gemm_prefill_w4a16_noalloc(const uint32_t* qweight, const uint16_t* scales,
@@ -1126,7 +1220,7 @@ extern "C" int qe_launch_gemm_prefill_w4a16_noalloc(const uint32_t* qweight, con
     p.M = M;
     p.N = N;
     p.K = K;
-    return launch_gemm<kPlain>(p, stream, what, ws, kWsFloats);
+    return launch_gemm<kPlain>(p, stream, what, Workspace{ws, kWsFloats});
 }
 
 extern "C" int qe_gemm_prefill_plan(int M, int N, int K, int tiled, int* tile, int* slices) {
@@ -1180,7 +1274,7 @@ extern "C" int qe_launch_gemm_prefill_w4a16_tiled(const uint32_t* tiled_weight, 
     p.M = M;
     p.N = N;
     p.K = K;
-    return launch_gemm<kPlain>(p, stream, what, gemm_workspace(stream), kWsFloats, true);
+    return launch_gemm<kPlain>(p, stream, what, gemm_workspace(stream), true);
 }
 
 extern "C" int qe_launch_gemm_prefill_qkv_w4a16_tiled(const qe_qkv_view* view, const uint16_t* input_x, int M,
@@ -1216,7 +1310,7 @@ extern "C" int qe_launch_gemm_prefill_qkv_w4a16_tiled(const qe_qkv_view* view, c
     p.M = M;
     p.N = q_dim + 2 * kv_dim;
     p.K = in_features;
-    return launch_gemm<kQKV>(p, stream, what, gemm_workspace(stream), kWsFloats, true);
+    return launch_gemm<kQKV>(p, stream, what, gemm_workspace(stream), true);
 }
 
 extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled(const uint32_t* tiled_weight,
@@ -1239,7 +1333,7 @@ extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16_tiled(const uint
     p.M = M;
     p.N = 2 * intermediate_size;
     p.K = hidden_size;
-    return launch_gemm<kSwiglu>(p, stream, what, gemm_workspace(stream), kWsFloats, true);
+    return launch_gemm<kSwiglu>(p, stream, what, gemm_workspace(stream), true);
 }
 
 extern "C" int qe_launch_gemm_prefill_qkv_w4a16(const qe_qkv_view* view, const uint16_t* input_x, int M,
@@ -1273,7 +1367,7 @@ extern "C" int qe_launch_gemm_prefill_qkv_w4a16(const qe_qkv_view* view, const u
     p.M = M;
     p.N = q_dim + 2 * kv_dim;
     p.K = in_features;
-    return launch_gemm<kQKV>(p, stream, what, gemm_workspace(stream), kWsFloats);
+    return launch_gemm<kQKV>(p, stream, what, gemm_workspace(stream));
 }
 
 extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(const uint32_t* gate_up_qweight,
@@ -1296,7 +1390,7 @@ extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a16(const uint32_t* 
     p.M = M;
     p.N = 2 * intermediate_size;
     p.K = hidden_size;
-    return launch_gemm<kSwiglu>(p, stream, what, gemm_workspace(stream), kWsFloats);
+    return launch_gemm<kSwiglu>(p, stream, what, gemm_workspace(stream));
 }
 
 // ---- W4A8 prefill GEMM entry points --------------------------------------------------
@@ -1330,7 +1424,7 @@ extern "C" int qe_launch_gemm_prefill_w4a8(const uint32_t* qweight, const uint16
     p.M = M;
     p.N = N;
     p.K = K;
-    return launch_gemm_w4a8<kPlain>(p, stream, what, gemm_workspace(stream), kWsFloats);
+    return launch_gemm_w4a8<kPlain>(p, stream, what, gemm_workspace(stream));
 }
 
 extern "C" int qe_launch_gemm_prefill_qkv_w4a8(const qe_qkv_view* view, const int8_t* input_q8,
@@ -1366,7 +1460,7 @@ extern "C" int qe_launch_gemm_prefill_qkv_w4a8(const qe_qkv_view* view, const in
     p.M = M;
     p.N = q_dim + 2 * kv_dim;
     p.K = in_features;
-    return launch_gemm_w4a8<kQKV>(p, stream, what, gemm_workspace(stream), kWsFloats);
+    return launch_gemm_w4a8<kQKV>(p, stream, what, gemm_workspace(stream));
 }
 
 extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a8(const uint32_t* gate_up_qweight,
@@ -1391,5 +1485,5 @@ extern "C" int qe_launch_gemm_prefill_dual_gate_up_swiglu_w4a8(const uint32_t* g
     p.M = M;
     p.N = 2 * intermediate_size;
     p.K = hidden_size;
-    return launch_gemm_w4a8<kSwiglu>(p, stream, what, gemm_workspace(stream), kWsFloats);
+    return launch_gemm_w4a8<kSwiglu>(p, stream, what, gemm_workspace(stream));
 }

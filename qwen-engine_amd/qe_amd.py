@@ -62,6 +62,8 @@ OTHER_SIGNATURES = {
     "qe_stream_read": [_P, ctypes.c_size_t, _P, _P],
     "qe_set_tuning": [ctypes.c_char_p, _I],
     "qe_gemm_reserve_workspace": [_P],
+    "qe_gemm_attach_workspace": [_P, _P, ctypes.c_size_t],
+    "qe_gemm_release_workspace": [_P],
     "qe_w4_tiled_bytes": [_I, _I, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
     "qe_repack_w4_tiled": [_P, _P, _I, _I, _P, _P, _P],
     "qe_gemm_prefill_plan": [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)],
@@ -123,6 +125,8 @@ def lib():
         L.qe_engine_destroy.restype = None
         L.qe_engine_default_config.argtypes = [_P]
         L.qe_engine_default_config.restype = None
+        L.qe_gemm_workspace_allocations.argtypes = []
+        L.qe_gemm_workspace_allocations.restype = ctypes.c_long
         L.qe_last_error.restype = ctypes.c_char_p
         L.qe_version.restype = ctypes.c_char_p
         _lib = L
@@ -521,7 +525,24 @@ def stream_read(data, nbytes: int, sink, stream=None):
 
 
 def gemm_reserve_workspace(stream=None):
+    """qe_gemm_reserve_workspace: a 32 MiB split-K workspace for the stream
+    (the only allocation of the kernel API; prefill GEMMs on a stream
+    without one run without K slices)."""
     _check(lib().qe_gemm_reserve_workspace(_stream(stream)), "qe_gemm_reserve_workspace")
+
+
+def gemm_attach_workspace(buf, nbytes: int, stream=None):
+    """qe_gemm_attach_workspace: caller memory as the stream's workspace."""
+    _check(lib().qe_gemm_attach_workspace(_stream(stream), _ptr(buf), nbytes), "qe_gemm_attach_workspace")
+
+
+def gemm_release_workspace(stream=None):
+    _check(lib().qe_gemm_release_workspace(_stream(stream)), "qe_gemm_release_workspace")
+
+
+def gemm_workspace_allocations() -> int:
+    """hipMalloc calls made so far for GEMM workspaces (test hook)."""
+    return int(lib().qe_gemm_workspace_allocations())
 
 
 def gemm_prefill_plan(M, N, K, tiled=False):

@@ -11,7 +11,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def _declared(header="qe_kernels.h"):
     text = open(os.path.join(ROOT, "include", header)).read()
-    return sorted(set(re.findall(r"^(?:int|void|const char\*|const uint16_t\*)\s+(qe_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int|long|void|const char\*|const uint16_t\*)\s+(qe_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_entry_points():
@@ -46,6 +46,21 @@ def test_bad_k_rejected_on_host(K):
     assert "multiple of 128" in L.qe_last_error().decode()
     rc = L.qe_launch_gemm_prefill_w4a16(16, 16, 16, None, 16, 4, 4, K, None, 0)
     assert rc == 1
+
+
+def test_gemm_workspace_calls_rejected_on_host():
+    """The per-thread stream handle never holds a split-K workspace, a NULL or
+    unaligned workspace is refused, and no workspace has been allocated: all
+    decided before any HIP call."""
+    import qe_amd
+    L = qe_amd.lib()
+    per_thread = 2  # hipStreamPerThread
+    assert L.qe_gemm_reserve_workspace(per_thread) == 1
+    assert "hipStreamPerThread" in L.qe_last_error().decode()
+    assert L.qe_gemm_attach_workspace(None, None, 1 << 25) == 1
+    assert L.qe_gemm_attach_workspace(None, 0x1000 + 16, 1 << 25) == 1
+    assert L.qe_gemm_attach_workspace(None, 0x1000, 1 << 10) == 1
+    assert qe_amd.gemm_workspace_allocations() == 0
 
 
 def test_null_pointers_rejected_on_host():

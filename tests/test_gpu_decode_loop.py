@@ -331,6 +331,51 @@ def test_engine_tiled_prefill_matches_qwenbin_layout(qe):
     assert outs[0][3] == outs[1][3]
 
 
+def test_engine_multi_chunk_prefill_equals_single_chunk(qe):
+    """Prefill in 64-token chunks (later chunks attend to the KV the earlier
+    ones wrote, positions rebased, src/engine.cu:529-590) against one 256-token
+    chunk.  With one GEMM plan forced (a row's arithmetic then does not depend
+    on M) the last residual row, the logits, the first token and the decode
+    tokens after it are bit-identical; with each engine's own plan the last
+    row differs from the forced result only by fp32 rounding (1 % of its
+    largest element)."""
+    n = 200
+    prompt = [(i * 7919) % 4096 for i in range(n)]
+    H = 1536
+
+    def run(chunk, forced):
+        cfg = _small_cfg(qe)
+        cfg.prefill_chunk = chunk
+        e = qe.Engine(cfg, seed=13)
+        if forced:
+            qe.set_tuning("gemm_tile", 4)
+            qe.set_tuning("gemm_slices", 1)
+        try:
+            t = e.prefill(prompt)
+        finally:
+            qe.set_tuning("gemm_tile", 0)
+            qe.set_tuning("gemm_slices", 0)
+        rows = (n - 1) % chunk + 1  # rows of the last chunk in the hidden buffer
+        last = e.read("hidden", np.float16, rows * H).reshape(rows, H)[rows - 1].copy()
+        lg = e.logits().copy()
+        dec = e.decode(8)
+        e.close()
+        return t, last, lg, dec
+
+    f64, f256 = run(64, True), run(256, True)
+    assert f64[0] == f256[0]
+    assert np.array_equal(f64[1].view(np.uint16), f256[1].view(np.uint16))
+    assert np.array_equal(f64[2].view(np.uint16), f256[2].view(np.uint16))
+    assert f64[3] == f256[3]
+    p64, p256 = run(64, False), run(256, False)
+    from helpers import ulp16
+    for got in (p64, p256):
+        assert np.all(np.isfinite(got[1].astype(np.float32)))
+        err = np.abs(got[1].astype(np.float64) - f64[1].astype(np.float64))
+        scale = np.abs(f64[1].astype(np.float64)).max()
+        assert err.max() <= 1e-2 * scale + 4 * ulp16(scale), err.max()
+
+
 @pytest.mark.parametrize("full", [False, True])
 def test_engine_arena_buffers_do_not_overlap(qe, full):
     """Every buffer carved out of the engine's arena (weights, tiled copies,

@@ -3,9 +3,9 @@
 Reference: src/kernels/gemm_prefill.cu (kernels :319-610, launchers
 :616-684).  fp16 A, fp16 dequantized W, fp32 accumulation, fp16 output;
 residual added as fp16(fp16(acc) + res).  Tolerance: helpers.assert_fp16_close.
-At the full BASELINE configs[3] sizes (M = 512, 1024) the double-precision
-oracle is too slow on the CPU, so the reference there is a plain PyTorch
-fp32 matmul of the oracle-dequantized weights (floating-point kernel).
+At the full BASELINE configs[3] sizes (M = 512, 1024) the oracle checks 16
+full rows of each output (the double-precision oracle over all M rows would
+take minutes on the CPU).
 """
 import numpy as np
 import pytest
@@ -20,6 +20,7 @@ pytestmark = pytest.mark.gpu
 def qe():
     import qe_amd
     qe_amd.lib()
+    qe_amd.gemm_reserve_workspace()  # split-K partials of the default stream's GEMMs
     return qe_amd
 
 
@@ -146,27 +147,24 @@ def test_gemm_every_tile_ragged(qe, orc, K):
         qe.set_tuning("gemm_slices", 0)
 
 
-def _torch_ref(orc, qw, sc, A, N, K):
-    wdq = torch.from_numpy(orc.dequant_w4_f16(qw, sc, N, K)).cuda().float()
-    a = torch.from_numpy(A).cuda().float()
-    acc = (a @ wdq.T).double()
-    bound = (a.abs() @ wdq.abs().T).double()
-    return acc.cpu().numpy(), bound.cpu().numpy()
-
-
 @pytest.mark.parametrize("M", [512, 1024])
 @pytest.mark.parametrize("N,K", [(2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960)])
 def test_gemm_full_configs(qe, orc, M, N, K):
-    """configs[3] at full size: fp32 torch matmul of the dequantized weights."""
+    """configs[3] at full size against the oracle: 16 full output rows spread
+    over every M tile (first, last, and rows in between), all N columns, with
+    the path's plain tolerance; every output row is finite."""
     print(f"gemm full M={M} N={N} K={K}", flush=True)
     qw, sc = orc.synth_w4(N + K, N, K)
     A = _A(orc, M, K, M)
     out = empty((M, N), torch.float16)
     qe.launch_gemm_prefill_w4a16(dev(qw), dev(sc), dev(A), None, out, M, N, K)
-    ex, bd = _torch_ref(orc, qw, sc, A, N, K)
-    # the fp32 torch reference itself carries ~K*2^-24*bound error: widen the floor
-    assert_fp16_close(host(out), ex, bd * 4, ex.astype(np.float32).astype(np.float16), min_identical=0.9,
-                      what="gemm full")
+    got = host(out)
+    assert np.all(np.isfinite(got.astype(np.float32)))
+    rows = sorted(set([0, 1, 63, 64, 127, 128, M // 2 - 1, M // 2, M // 2 + 37, M - 129, M - 128, M - 65,
+                       M - 64, M - 2, M - 1, 200]))
+    assert len(rows) == 16
+    ref, ex, bd = orc.gemm_w4a16(qw, sc, A[rows], len(rows), N, K)
+    assert_fp16_close(got[rows], ex, bd, ref, what=f"gemm full {M}x{N}x{K}")
 
 
 def test_gemm_rejects_bad_k(qe):
@@ -284,6 +282,8 @@ def test_gemm_split_k_streams_do_not_share_partials(qe, orc):
         fn(o, None)
         alone.append(host(o))
     s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    qe.gemm_reserve_workspace(s1)
+    qe.gemm_reserve_workspace(s2)
     for _ in range(3):
         o1, o2 = empty((M, I), torch.float16), empty((M, H), torch.float16)
         torch.cuda.synchronize()
@@ -298,20 +298,29 @@ def test_gemm_split_k_streams_do_not_share_partials(qe, orc):
     assert_fp16_close(alone[1][:8], ex, bd, ref, what="down M=128 rows 0..7")
 
 
-def test_gemm_captured_without_workspace_matches_tolerance(qe, orc):
-    """A GEMM captured into a graph on a stream that never ran one eagerly has
-    no workspace (no allocation under capture) and runs without K slices;
-    after qe_gemm_reserve_workspace it splits again.  Both stay within the
-    oracle tolerance and replays repeat bit for bit."""
+def test_gemm_launch_never_allocates_and_plan_depends_only_on_the_stream(qe, orc):
+    """A prefill GEMM on a fresh stream makes no hipMalloc (the library's
+    workspace allocation counter does not move) and runs without K slices;
+    captured into a graph on another fresh stream it gives the same bits.
+    After qe_gemm_reserve_workspace (one allocation) the stream splits K, and
+    eager and captured launches on it agree bit for bit again.  Every result
+    is within the oracle tolerance."""
     M, N, K = 128, 1536, 8960
+    assert qe.gemm_prefill_plan(M, N, K)[1] > 1  # this shape splits when it can
     qw, sc = orc.synth_w4(51, N, K)
     A = _A(orc, M, K, 52)
     dq, ds, dA = dev(qw), dev(sc), dev(A)
     ref, ex, bd = orc.gemm_w4a16(qw, sc, A[:16], 16, N, K)
-    for reserve in (False, True):
-        s = torch.cuda.Stream()
-        if reserve:
-            qe.gemm_reserve_workspace(s)
+    torch.cuda.synchronize()
+
+    def eager(s):
+        out = empty((M, N), torch.float16)
+        torch.cuda.synchronize()
+        qe.launch_gemm_prefill_w4a16(dq, ds, dA, None, out, M, N, K, stream=s)
+        torch.cuda.synchronize()
+        return host(out).copy()
+
+    def captured(s):
         out = empty((M, N), torch.float16)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=s):
@@ -323,7 +332,37 @@ def test_gemm_captured_without_workspace_matches_tolerance(qe, orc):
             torch.cuda.synchronize()
             outs.append(host(out).copy())
         assert all(np.array_equal(o.view(np.uint16), outs[0].view(np.uint16)) for o in outs)
-        assert_fp16_close(outs[0][:16], ex, bd, ref, what=f"captured gemm reserve={reserve}")
+        return outs[0]
+
+    before = qe.gemm_workspace_allocations()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    unsplit = eager(s1)
+    assert qe.gemm_workspace_allocations() == before, "a launch allocated"
+    assert np.array_equal(captured(s2).view(np.uint16), unsplit.view(np.uint16))
+    assert qe.gemm_workspace_allocations() == before, "a captured launch allocated"
+    assert np.array_equal(eager(s1).view(np.uint16), unsplit.view(np.uint16))
+    # the unsplit plan is the forced single-slice plan on a stream with a workspace
+    qe.set_tuning("gemm_slices", 1)
+    try:
+        assert np.array_equal(eager(None).view(np.uint16), unsplit.view(np.uint16))
+    finally:
+        qe.set_tuning("gemm_slices", 0)
+    assert_fp16_close(unsplit[:16], ex, bd, ref, what="gemm without workspace")
+    qe.gemm_reserve_workspace(s1)
+    assert qe.gemm_workspace_allocations() == before + 1
+    qe.gemm_reserve_workspace(s1)  # idempotent
+    assert qe.gemm_workspace_allocations() == before + 1
+    split = eager(s1)
+    assert np.array_equal(captured(s1).view(np.uint16), split.view(np.uint16))
+    assert_fp16_close(split[:16], ex, bd, ref, what="gemm with workspace")
+    # caller memory as the workspace gives the same plan and bits
+    buf = torch.empty(32 << 20, dtype=torch.uint8, device="cuda")
+    qe.gemm_attach_workspace(buf, buf.numel(), s2)
+    assert np.array_equal(eager(s2).view(np.uint16), split.view(np.uint16))
+    qe.gemm_release_workspace(s2)
+    qe.gemm_release_workspace(s1)
+    assert np.array_equal(eager(s1).view(np.uint16), unsplit.view(np.uint16))
+    assert qe.gemm_workspace_allocations() == before + 1
 
 
 # ---- tiled weight layout (load-time repack) ----------------------------------------

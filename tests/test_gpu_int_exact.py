@@ -29,6 +29,7 @@ DENSE = dict(sparse=False, act_exps=(0, 1), w_exps=(2, 3, 4))
 def qe():
     import qe_amd
     qe_amd.lib()
+    qe_amd.gemm_reserve_workspace()  # split-K partials of the default stream's GEMMs
     return qe_amd
 
 

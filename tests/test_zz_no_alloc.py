@@ -17,6 +17,7 @@ pytestmark = pytest.mark.gpu
 def qe():
     import qe_amd
     qe_amd.lib()
+    qe_amd.gemm_reserve_workspace()  # split-K partials of the default stream's GEMMs
     return qe_amd
 
 
