@@ -4,7 +4,14 @@
  * the packed .qwenbin layout (uint32 [N][K/8] nibbles, fp16 [N][K/128]
  * scales, LM head tied to the embedding) or loaded from a .qwenbin v2 file
  * (include/qwenbin.h).  One engine = one HIP stream, one device arena
- * (allocated at create), one captured decode graph.
+ * (allocated at create), one captured decode graph.  Besides the weights
+ * (or the .qwenbin payload, one device copy), the KV cache and the
+ * activations, the arena holds a 32 MiB split-K workspace for the prefill
+ * GEMMs (registered for the engine's stream) and, unless
+ * qe_set_tuning("engine_tiled_prefill", 0) was set before create, a tiled
+ * copy of every layer matrix for the prefill GEMMs (+0.75 GB at
+ * Qwen2.5-1.5B: about 0.8x the layer weights).  The switch is read once at
+ * create.  qe_engine_arena_spans reports the arena's size.
  *
  * Counterpart of the reference's QwenEngine (include/engine.cuh:104-226):
  * construction from a .qwenbin (load_model_file + setup_arena), prefill
