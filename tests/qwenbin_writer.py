@@ -16,12 +16,28 @@ HEADER_FMT = "<12I2f2I11Q"
 LAYER_FMT = "<2I26Q"
 
 
-def synth_model(L=2, H=256, I=256, nq=2, nkv=1, V=512, seed=0, untied=False):
-    """Random tensors of a small GQA model in the packed W4A16 G128 layout."""
+def center_nibbles(w: np.ndarray) -> np.ndarray:
+    """Every zero nibble of the packed words becomes 8: uniform nibbles in
+    [0, 15] then have mean exactly 8 (the zero point), i.e. weights with no
+    common-mode term."""
+    t = w | (w >> 1)
+    t |= t >> 2
+    zero = ~t & np.uint32(0x11111111)  # bit 0 of each nibble that is 0
+    return w | (zero << 3)
+
+
+def synth_model(L=2, H=256, I=256, nq=2, nkv=1, V=512, seed=0, untied=False, centered=False):
+    """Random tensors of a small GQA model in the packed W4A16 G128 layout.
+    centered: layer weights with nibble mean 8 (center_nibbles), scales
+    |N(0,1)| / sqrt(17.5 K) (the variance of such a weight is 17.5 s^2)."""
     rng = np.random.default_rng(seed)
     qd, kvd = nq * 128, nkv * 128
 
     def mat(N, K):
+        if centered:
+            w = center_nibbles(np.frombuffer(rng.bytes(N * K // 2), np.uint32).reshape(N, K // 8))
+            s = (np.abs(rng.standard_normal((N, K // 128))) / np.sqrt(17.5 * K)).astype(np.float16)
+            return w, s
         w = rng.integers(0, 2 ** 32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32)
         s = (np.abs(rng.standard_normal((N, K // 128))) / np.sqrt(21.5 * K)).astype(np.float16)
         return w, s

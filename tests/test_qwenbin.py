@@ -103,3 +103,18 @@ def test_truncated_and_missing_files(qe, tmp_path):
     open(p, "wb").write(data[:100])
     _expect_fail(qe, p, None, "too small")
     _expect_fail(qe, tmp_path / "absent.qwenbin", None, "cannot open")
+
+
+def test_center_nibbles_maps_zero_to_eight_only():
+    """The centered test weights: every nibble 0 becomes 8, every other nibble
+    is kept, so uniform nibbles get mean exactly 8 (the zero point)."""
+    import numpy as np
+    import qwenbin_writer as qw
+    w = np.random.default_rng(1).integers(0, 2 ** 32, size=20000, dtype=np.uint64).astype(np.uint32)
+    w[:16] = [0, 0xFFFFFFFF, 0x0F0F0F0F, 0xF0F0F0F0, 0x10000000, 1, 0x88888888, 0x01234567] * 2
+    c = qw.center_nibbles(w)
+    nib = lambda a: np.stack([(a >> (4 * j)) & 15 for j in range(8)])
+    o, n = nib(w), nib(c)
+    assert np.array_equal(n, np.where(o == 0, 8, o))
+    assert c[0] == 0x88888888 and c[1] == 0xFFFFFFFF and c[2] == 0x8F8F8F8F
+    assert abs(n.mean() - 8.0) < 0.02
