@@ -121,7 +121,7 @@ __device__ __forceinline__ uint4 rms_apply8(uint4 xv, uint4 gv, _Float16 h) {
 // VEC: 16-byte vector loads are legal for the activation buffers.
 // kXRMS: s_units holds K / 8 floats for the sum of squares.
 template <int XM, int BT, bool VEC>
-__device__ __forceinline__ void stage_activation(const GemvParams& p, int8_t* s_q8, int2* s_rec, float* s_red,
+__device__ __forceinline__ void stage_activation(const GemvParams& p, int8_t* s_q8, int2* s_rec,
                                                  float* s_units) {
     const int K = p.K;
     const int G = K >> 7;
@@ -140,7 +140,7 @@ __device__ __forceinline__ void stage_activation(const GemvParams& p, int8_t* s_
         _Float16 h = static_cast<_Float16>(0.0f);
         if constexpr (XM == kXRMS) {
             for (int i = threadIdx.x; i < (K >> 3); i += BT) s_units[i] = rms_unit_sq(load8_f16(p.x16 + 8 * i, VEC));
-            h = rms_inv_f16(s_units, K >> 3, K, kRmsEps, s_red);
+            h = rms_inv_f16_each_wave(s_units, K >> 3, K, kRmsEps);
         }
         const int sub = threadIdx.x & 15;
         for (int g = threadIdx.x >> 4; g < G; g += BT / 16) {
@@ -304,7 +304,7 @@ __device__ __forceinline__ void stage_issue_f16(const GemvParams& p, uint4 (&raw
 
 template <int XM, int BT, int MAXP>
 __device__ __forceinline__ void stage_finish_f16(const GemvParams& p, uint4 (&raw)[MAXP], const uint4 (&graw)[MAXP],
-                                                 int8_t* s_q8, int2* s_rec, float* s_red, float* s_units) {
+                                                 int8_t* s_q8, int2* s_rec, float* s_units) {
     const int K = p.K;
     const int U = K >> 3;  // 8-element units
     const int t = threadIdx.x;
@@ -312,7 +312,7 @@ __device__ __forceinline__ void stage_finish_f16(const GemvParams& p, uint4 (&ra
 #pragma unroll
         for (int j = 0; j < MAXP; ++j)
             if (t + BT * j < U) s_units[t + BT * j] = rms_unit_sq(raw[j]);
-        const _Float16 h = rms_inv_f16(s_units, U, K, kRmsEps, s_red);
+        const _Float16 h = rms_inv_f16_each_wave(s_units, U, K, kRmsEps);
         const bool write_norm = p.norm_out != nullptr && blockIdx.x == 0;
 #pragma unroll
         for (int j = 0; j < MAXP; ++j) {
@@ -540,12 +540,11 @@ __device__ __forceinline__ void gemv_w4_body(const GemvParams& p) {
     // ---- activation slice in VGPRs, through LDS ----------------------------------
     {
         extern __shared__ __align__(16) uint8_t s_mem[];
-        __shared__ float s_red[BT / 64];
         int8_t* s_q8 = reinterpret_cast<int8_t*>(s_mem);
         int2* s_rec = reinterpret_cast<int2*>(s_mem + K);
         if constexpr (XM == kXQ8) stage_finish_q8<BT, MQ>(p, qa, qb, qs4, qxd, s_q8, s_rec);
         else if constexpr (is_attn(XM)) stage_finish_attn<LS>(p, apo, apl, s_q8, s_rec);
-        else stage_finish_f16<XM, BT, MAXP>(p, raw, graw, s_q8, s_rec, s_red,
+        else stage_finish_f16<XM, BT, MAXP>(p, raw, graw, s_q8, s_rec,
                                             reinterpret_cast<float*>(s_mem + K + (K >> 5) * 8 + 32));
         __syncthreads();
 #pragma unroll
@@ -711,12 +710,11 @@ __global__ __launch_bounds__(256) void gemv_attn_o_kernel(GemvParams) {
 template <int MODE, int XM>
 __global__ __launch_bounds__(256) void gemv_w4_generic_kernel(GemvParams p) {
     extern __shared__ __align__(16) uint8_t s_mem[];
-    __shared__ float s_red[4];
     const int K = p.K;
     const int KW = K >> 3;
     int8_t* s_q8 = reinterpret_cast<int8_t*>(s_mem);
     int2* s_rec = reinterpret_cast<int2*>(s_mem + K);
-    stage_activation<XM, 256, false>(p, s_q8, s_rec, s_red, reinterpret_cast<float*>(s_mem + K + (K >> 5) * 8));
+    stage_activation<XM, 256, false>(p, s_q8, s_rec, reinterpret_cast<float*>(s_mem + K + (K >> 5) * 8));
     __syncthreads();
     const int wave = threadIdx.x >> 6;
     const int l = threadIdx.x & 63;

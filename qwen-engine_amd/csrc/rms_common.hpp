@@ -10,7 +10,8 @@
 //     for e = 1..7;
 //   * lane l of wave 0 adds s_l, s_{l+64}, s_{l+128}, ... in that order;
 //   * the 64 lane sums meet through the xor butterfly of seg_sum<64>.
-// Kernels store their units' s_u in LDS and call rms_inv_f16.
+// Kernels store their units' s_u in LDS and call rms_inv_f16 or
+// rms_inv_f16_each_wave.
 #pragma once
 
 #include "qe_common.hpp"
@@ -44,6 +45,20 @@ __device__ __forceinline__ _Float16 rms_inv_f16(const float* s_units, int U, int
     }
     __syncthreads();
     const float inv_rms = 1.0f / sqrtf(*s_total / static_cast<float>(H) + eps);
+    return static_cast<_Float16>(inv_rms);
+}
+
+// The same value with one barrier: every wave sums the units itself in the
+// order above (lane l: s_l, s_{l+64}, ...; then the butterfly), so all waves
+// hold the wave-0 result bit for bit and nothing is broadcast through LDS.
+// The caller must not overwrite s_units afterwards without a barrier.
+__device__ __forceinline__ _Float16 rms_inv_f16_each_wave(const float* s_units, int U, int H, float eps) {
+    __syncthreads();
+    const int l = threadIdx.x & 63;
+    float p = 0.0f;
+    for (int u = l; u < U; u += 64) p += s_units[u];
+    p = qwen::seg_sum<64>(p);
+    const float inv_rms = 1.0f / sqrtf(p / static_cast<float>(H) + eps);
     return static_cast<_Float16>(inv_rms);
 }
 
