@@ -343,13 +343,12 @@ extern "C" void qe_engine_destroy(qe_engine* e) {
     if (e == nullptr) return;
     if (e->graph_exec) (void)hipGraphExecDestroy(e->graph_exec);
     if (e->graph) (void)hipGraphDestroy(e->graph);
+    // the stream's workspace registration goes before the arena that holds it
+    if (e->stream && e->gemm_ws) (void)qe_gemm_release_workspace(e->stream);
     if (e->h_token) (void)hipHostFree(e->h_token);
     if (e->arena) (void)hipFree(e->arena);
     if (e->payload) (void)hipFree(e->payload);
-    if (e->stream) {
-        if (e->gemm_ws) (void)qe_gemm_release_workspace(e->stream);
-        (void)hipStreamDestroy(e->stream);
-    }
+    if (e->stream) (void)hipStreamDestroy(e->stream);
     delete e;
 }
 
