@@ -376,6 +376,25 @@ def test_engine_multi_chunk_prefill_equals_single_chunk(qe):
         assert err.max() <= 1e-2 * scale + 4 * ulp16(scale), err.max()
 
 
+def test_engine_destroy_releases_its_gemm_workspace(qe):
+    """Every engine registers 32 MiB of its arena as its stream's split-K
+    workspace (at most 64 streams per device hold one) and drops the
+    registration at destroy: 70 engines created and destroyed in turn all
+    succeed, none allocates a library workspace, and the last one still
+    prefills with split K (same first token as the first engine)."""
+    before = qe.gemm_workspace_allocations()
+    prompt = [(i % 1000) + 100 for i in range(100)]
+    first = None
+    for i in range(70):
+        e = qe.Engine(_small_cfg(qe), seed=21)
+        if i in (0, 69):
+            t = e.prefill(prompt)
+            first = t if first is None else first
+            assert t == first
+        e.close()
+    assert qe.gemm_workspace_allocations() == before
+
+
 @pytest.mark.parametrize("full", [False, True])
 def test_engine_arena_buffers_do_not_overlap(qe, full):
     """Every buffer carved out of the engine's arena (weights, tiled copies,
