@@ -363,6 +363,26 @@ def test_suite3_generator_matches_mt19937_recipe(orc):
     assert np.all(sc == np.float16(np.float32(0.05) * sf))
 
 
+def test_suite3_nibbles_match_lemire_draws(orc):
+    """The Suite 3 nibbles bit for bit: std::uniform_int_distribution<int>(2, 14)
+    on a 32-bit mt19937 is, in libstdc++ 11 (bits/uniform_int_dist.h, _S_nd),
+    Lemire's nearly divisionless method - q = 2 + (x * 13) >> 32 for each
+    32-bit draw x, redrawing only when (x * 13) mod 2^32 < 2^32 mod 13 (never
+    in these draws) - one draw per nibble after the H draws of x, nibbles
+    q0..q7 of a word in draw order (tests/test_kernels.cu:288-300).  (A
+    libstdc++ older than 11 divides instead and would give other nibbles.)"""
+    for H, I in ((256, 512), (1536, 256)):
+        _, qw, _ = orc.suite3_inputs(H, I)
+        words = 2 * I * (H // 8)
+        raw = np.random.RandomState(42 + H).randint(0, 2 ** 32, size=H + 8 * words, dtype=np.uint32)
+        prod = raw[H:].astype(np.uint64) * np.uint64(13)
+        assert np.all((prod & np.uint64(0xFFFFFFFF)) >= np.uint64((2 ** 32) % 13))  # no redraw happened
+        qd = (2 + (prod >> np.uint64(32))).astype(np.uint32).reshape(words, 8)
+        packed = (qd[:, 0] | (qd[:, 4] << 4) | (qd[:, 1] << 8) | (qd[:, 5] << 12) | (qd[:, 2] << 16) |
+                  (qd[:, 6] << 20) | (qd[:, 3] << 24) | (qd[:, 7] << 28)).astype(np.uint32)
+        assert np.array_equal(qw.reshape(-1), packed)
+
+
 def test_synth_distributions(orc):
     qw, sc = orc.synth_w4(123, 256, 1536)
     q = _unpack_np(qw, 256, 1536)
